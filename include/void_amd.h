@@ -1,0 +1,166 @@
+/*
+ * void_amd.h — C ABI of the MI355X (gfx950) quantized block-sparse SpMM library.
+ *
+ * The library replaces the Triton launches of the reference's quantized SpMM
+ * path.  Every entry point takes plain device pointers and sizes, launches
+ * asynchronously on the caller's HIP stream, never allocates or frees device
+ * memory, and returns 0 on success or a negative void_status code (the text
+ * of the last error is available from void_last_error()).
+ *
+ * Sparse operand A ("BSR view" of a VOID tensor): 32x32 tiles stored
+ * block-row-major — tiles of block-row r occupy [row_ptr[r], row_ptr[r+1])
+ * with ascending block column — so that a workgroup streams one block-row's
+ * tiles from contiguous HBM.  This is the order the reference visits tiles
+ * in (Int8VOIDTensor.get_row_block_info, void/int_quant.py:158-175), with the
+ * block_indices indirection resolved once at conversion time.
+ *
+ * Dense operand B is int8 (INT8 path) or fp8 E4M3FN (FP8 path), K x N,
+ * either row-major (element (k,n) at b[k*ldb+n], the reference's layout) or
+ * column-major (element (k,n) at b[n*ldb+k]).
+ */
+#ifndef VOID_AMD_H
+#define VOID_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VOID_AMD_ABI_VERSION 1
+#define VOID_TILE 32
+
+typedef enum void_status {
+  VOID_OK = 0,
+  VOID_ERR_ARG = -1,         /* null pointer, negative size, shape mismatch */
+  VOID_ERR_UNSUPPORTED = -2, /* combination not implemented (e.g. row_mean on fp8) */
+  VOID_ERR_HIP = -3,         /* a HIP runtime call failed */
+  VOID_ERR_WORKSPACE = -4,   /* workspace missing or too small for the plan */
+  VOID_ERR_CAPACITY = -5     /* planner output array too small */
+} void_status;
+
+/* Epilogue applied to the int32 / fp32 accumulators of one 32 x N tile. */
+typedef enum void_epilogue {
+  /* int32 accumulators of the whole block-row, stored raw (out_dtype must be I32). */
+  VOID_EPI_RAW_I32 = 0,
+  /* Reference semantics of void_spmm_int8_kernel (void/int_quant.py:519-526):
+   *   S = sequential fp32 sum over the row's tiles (ascending column) of fl(s_a[t] * s_b)
+   *   C = f32(acc_i32) * (S / n_tiles_in_row), 0 for an empty row. */
+  VOID_EPI_ROW_MEAN = 1,
+  /* True per-tile dequantisation: C = s_b * sum_t s_a[t] * f32(A_t @ B_t). */
+  VOID_EPI_PER_BLOCK = 2
+} void_epilogue;
+
+typedef enum void_dtype {
+  VOID_DT_F32 = 0,
+  VOID_DT_BF16 = 1,
+  VOID_DT_F16 = 2,
+  VOID_DT_I32 = 3
+} void_dtype;
+
+/* Activation codes follow get_activation_code (void/fusion.py:77-91). */
+typedef enum void_activation {
+  VOID_ACT_NONE = 0,
+  VOID_ACT_RELU = 1,
+  VOID_ACT_GELU = 2, /* tanh form, void/fusion.py:38-43 */
+  VOID_ACT_SILU = 3
+} void_activation;
+
+/* Device view of a quantized VOID tensor (Int8VOIDTensor / FP8VOIDTensor). */
+typedef struct void_bsr_desc {
+  const void* tiles;      /* [n_blocks][32][32] int8 or e4m3fn bytes, block-row-major */
+  const float* scales;    /* [n_blocks] per-tile scale (same order), or [1] if per_tensor_a */
+  const int32_t* row_ptr; /* [n_block_rows + 1] */
+  const int32_t* col_idx; /* [n_blocks] block column of each tile */
+  int32_t M, K;           /* dense shape of A */
+  int32_t n_blocks;
+  int32_t n_block_rows;   /* ceil(M / 32) */
+  int32_t per_tensor_a;   /* 1: scales[0] applies to every tile */
+  int32_t reserved;
+} void_bsr_desc;
+
+/* One unit of work: tiles [begin, end) of block-row `row`.  A row with more
+ * tiles than the plan's chunk size is split into `nchunks` items that each
+ * write a partial tile into workspace slot (slot + chunk); the last of them
+ * to finish (counted on split tile `tile`) reduces the partials in chunk
+ * order and applies the epilogue.  tile == -1 marks an unsplit row.
+ * Replaces StreamKWorkload (void/stream_k.py:13-33). */
+typedef struct void_work_item {
+  int32_t row, begin, end, tile;
+  int32_t nchunks, chunk, slot, reserved;
+} void_work_item;
+
+/* A plan from void_streamk_plan with its items copied to device memory. */
+typedef struct void_plan {
+  const void_work_item* items; /* device array of n_items entries */
+  int32_t n_items;
+  int32_t n_split_tiles;
+  int32_t n_slots;
+  int32_t chunk_tiles;
+} void_plan;
+
+/* The dense operand and the output of one SpMM call. */
+typedef struct void_dense_args {
+  const void* b;          /* K x N int8 / e4m3fn */
+  int64_t ldb;            /* elements between consecutive rows (row-major) or columns (column-major) */
+  int32_t b_col_major;    /* 0: (k,n) at b[k*ldb+n]; 1: (k,n) at b[n*ldb+k] */
+  int32_t N;
+  float b_scale;          /* per-tensor scale of B, used when b_scale_vec is NULL */
+  const float* b_scale_vec; /* [N] per-column scale of B, or NULL */
+  const float* bias;      /* [N] added before the activation, or NULL */
+  void* c;                /* M x N row-major output */
+  int64_t ldc;
+  int32_t out_dtype;      /* void_dtype */
+  int32_t activation;     /* void_activation */
+} void_dense_args;
+
+/* ---------------------------------------------------------------------- */
+
+/* ABI version (VOID_AMD_ABI_VERSION) of the loaded library. */
+int void_abi_version(void);
+
+/* Text of the last error reported on the calling thread ("" if none). */
+const char* void_last_error(void);
+
+/* Width in columns of the N panel one workgroup computes (128). */
+int void_panel_width(void);
+
+/* Host-side Stream-K planner.  Replaces compute_stream_k_workload
+ * (void/stream_k.py:36-110): every block-row becomes one item, except rows
+ * with more than chunk_tiles tiles, which are split into ceil(n/chunk_tiles)
+ * near-equal chunks.  Items are ordered longest-first; empty rows are kept
+ * (they produce the zero / activation(bias) rows of C).
+ * row_ptr is a HOST array of n_block_rows + 1 entries.
+ * On VOID_ERR_CAPACITY, *n_items holds the required capacity. */
+int void_streamk_plan(const int32_t* row_ptr, int32_t n_block_rows, int32_t chunk_tiles,
+                      void_work_item* items, int32_t capacity, int32_t* n_items,
+                      int32_t* n_split_tiles, int32_t* n_slots);
+
+/* Bytes of device workspace a plan needs for N output columns (0 if the plan
+ * splits no row).  The first n_split_tiles * n_panels int32 counters of the
+ * workspace must be zero before the first launch; every launch leaves them
+ * zero again.  Calls that share one workspace must not overlap in time. */
+size_t void_workspace_bytes(int32_t n_split_tiles, int32_t n_slots, int32_t N);
+
+/* INT8 block-sparse SpMM, replacing void_spmm_int8_kernel + void_spmm_int8
+ * (void/int_quant.py:435-612) and, with activation != NONE, the INT8 form of
+ * void_spmm_activation_kernel (void/fusion.py:98-198).
+ * epilogue: void_epilogue; RAW_I32 requires out_dtype == I32.
+ * workspace: void_workspace_bytes(plan) bytes, NULL when the plan splits no row. */
+int void_spmm_int8(const void_bsr_desc* a, const void_dense_args* d, int32_t epilogue,
+                   const void_plan* plan, void* workspace, size_t workspace_bytes,
+                   hipStream_t stream);
+
+/* FP8 (E4M3FN x E4M3FN, fp32 accumulate) block-sparse SpMM, replacing
+ * void_spmm_fp8_kernel + void_spmm_fp8 (void/fp8.py:577-742).  The epilogue
+ * is always PER_BLOCK: C = s_b * sum_t s_a[t] * (A_t @ B_t). */
+int void_spmm_fp8(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
+                  void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VOID_AMD_H */

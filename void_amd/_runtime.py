@@ -1,0 +1,186 @@
+"""Device-side state shared by the quantized SpMM entry points.
+
+A quantized VOID tensor gets, once per device, a ``DeviceBsr``: its tiles and
+scales gathered into block-row-major order, the block-row pointer and column
+indices, and a cache of Stream-K plans (work items on the device plus a
+zero-initialised workspace).  ``launch`` fills the C-ABI descriptors and calls
+into ``libvoid_amd.so`` on the current torch stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+from typing import Dict, Optional, Tuple
+
+import numpy as np
+import torch
+
+from . import _lib
+from .format import build_bsr_layout
+
+_OUT_CODES = {
+    torch.float32: _lib.DT_F32,
+    torch.bfloat16: _lib.DT_BF16,
+    torch.float16: _lib.DT_F16,
+    torch.int32: _lib.DT_I32,
+}
+
+
+@dataclass
+class DevicePlan:
+    items: torch.Tensor          # int32 [n_items, 8] on device (void_work_item)
+    n_items: int
+    n_split_tiles: int
+    n_slots: int
+    chunk: int
+    host_items: np.ndarray       # int32 [n_items, 8] copy, for inspection
+    workspaces: Dict[int, torch.Tensor] = field(default_factory=dict)
+
+    def workspace(self, N: int, device: torch.device) -> Tuple[Optional[torch.Tensor], int]:
+        nbytes = int(_lib.lib().void_workspace_bytes(self.n_split_tiles, self.n_slots, N))
+        if nbytes == 0:
+            return None, 0
+        ws = self.workspaces.get(nbytes)
+        if ws is None:
+            # Counters must start at zero; every launch leaves them at zero.
+            ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+            self.workspaces[nbytes] = ws
+        return ws, nbytes
+
+
+def plan_rows(row_ptr_host: np.ndarray, chunk: int) -> Tuple[np.ndarray, int, int]:
+    """Run the C planner on a host row pointer; returns (items[n,8], n_split_tiles, n_slots)."""
+    lib = _lib.lib()
+    rp = np.ascontiguousarray(row_ptr_host, dtype=np.int32)
+    n_br = rp.size - 1
+    n_items = ctypes.c_int32()
+    n_tiles = ctypes.c_int32()
+    n_slots = ctypes.c_int32()
+    rp_ptr = rp.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+    cap = max(n_br, 1)
+    while True:
+        buf = (_lib.WorkItem * cap)()
+        st = lib.void_streamk_plan(rp_ptr, n_br, int(chunk), buf, cap, ctypes.byref(n_items),
+                                   ctypes.byref(n_tiles), ctypes.byref(n_slots))
+        if st == -5 and n_items.value > cap:
+            cap = n_items.value
+            continue
+        _lib.check(st, "void_streamk_plan")
+        break
+    items = np.frombuffer(buf, dtype=np.int32, count=n_items.value * 8).reshape(n_items.value, 8).copy()
+    return items, n_tiles.value, n_slots.value
+
+
+@dataclass
+class DeviceBsr:
+    tiles: torch.Tensor          # uint8 [n_blocks, 32, 32] block-row-major
+    scales: torch.Tensor         # float32 [n_blocks] (or [1] with per_tensor)
+    row_ptr: torch.Tensor        # int32 [n_block_rows + 1]
+    col_idx: torch.Tensor        # int32 [n_blocks]
+    row_ptr_host: np.ndarray
+    per_tensor: bool
+    M: int
+    K: int
+    n_blocks: int
+    n_block_rows: int
+    plans: Dict[int, DevicePlan] = field(default_factory=dict)
+
+    def plan(self, chunk: int) -> DevicePlan:
+        p = self.plans.get(chunk)
+        if p is None:
+            items, n_tiles, n_slots = plan_rows(self.row_ptr_host, chunk)
+            dev_items = torch.from_numpy(items).to(self.row_ptr.device)
+            p = DevicePlan(dev_items, items.shape[0], n_tiles, n_slots, chunk, items)
+            self.plans[chunk] = p
+        return p
+
+    def desc(self) -> _lib.BsrDesc:
+        return _lib.BsrDesc(
+            tiles=self.tiles.data_ptr() if self.n_blocks else None,
+            scales=self.scales.data_ptr() if self.scales.numel() else None,
+            row_ptr=self.row_ptr.data_ptr(),
+            col_idx=self.col_idx.data_ptr() if self.n_blocks else None,
+            M=self.M, K=self.K, n_blocks=self.n_blocks, n_block_rows=self.n_block_rows,
+            per_tensor_a=int(self.per_tensor), reserved=0)
+
+
+def make_device_bsr(values: torch.Tensor, scales: torch.Tensor, block_rows: torch.Tensor,
+                    block_cols: torch.Tensor, shape: Tuple[int, int], tile_size: Tuple[int, int],
+                    device: torch.device, per_tensor: bool) -> DeviceBsr:
+    if tuple(tile_size) != (32, 32):
+        raise NotImplementedError(f"the gfx950 kernels take 32x32 tiles, got {tile_size}")
+    M, K = shape
+    n_br = (M + 31) // 32
+    n_bc = (K + 31) // 32
+    lay = build_bsr_layout(block_rows, block_cols, n_br, n_bc, device)
+    v = values.to(device)
+    if v.dtype != torch.uint8:
+        v = v.view(torch.uint8)
+    tiles = v.index_select(0, lay.order).contiguous() if v.shape[0] else v.contiguous()
+    s = scales.to(device=device, dtype=torch.float32)
+    if per_tensor:
+        s = s.reshape(-1)[:1].contiguous()
+    else:
+        s = s.index_select(0, lay.order).contiguous() if s.numel() else s.contiguous()
+    return DeviceBsr(tiles=tiles, scales=s, row_ptr=lay.row_ptr, col_idx=lay.col_idx,
+                     row_ptr_host=lay.row_ptr_host, per_tensor=per_tensor, M=M, K=K,
+                     n_blocks=int(values.shape[0]), n_block_rows=n_br)
+
+
+def require_gpu(t: torch.Tensor, what: str) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{what} must be a GPU (HIP) tensor; the SpMM runs only on the gfx950 "
+                           f"kernels of libvoid_amd.so (got device {t.device})")
+
+
+def dense_operand(b: torch.Tensor) -> Tuple[torch.Tensor, int, bool]:
+    """(tensor, ld, col_major) for B without copying when B is row- or column-major."""
+    if b.stride(1) == 1 and (b.stride(0) >= b.shape[1] or b.shape[0] <= 1):
+        return b, max(b.stride(0), b.shape[1]), False
+    if b.stride(0) == 1 and (b.stride(1) >= b.shape[0] or b.shape[1] <= 1):
+        return b, max(b.stride(1), b.shape[0]), True
+    b = b.contiguous()
+    return b, b.shape[1], False
+
+
+def launch(kind: str, dbsr: DeviceBsr, b: torch.Tensor, *, b_scale: float = 1.0,
+           b_scale_vec: Optional[torch.Tensor] = None, out: torch.Tensor, epilogue: int,
+           activation: int = _lib.ACT_NONE, bias: Optional[torch.Tensor] = None,
+           chunk: int) -> torch.Tensor:
+    """Launch one SpMM on the current stream of out's device; returns out."""
+    lib = _lib.lib()
+    N = b.shape[1]
+    b_t, ldb, col_major = dense_operand(b)
+    target = out
+    if out.stride(1) != 1 or out.stride(0) < N:
+        target = torch.empty(out.shape, dtype=out.dtype, device=out.device)
+    plan = dbsr.plan(chunk)
+    ws, ws_bytes = plan.workspace(N, out.device)
+    cplan = _lib.Plan(items=plan.items.data_ptr(), n_items=plan.n_items,
+                      n_split_tiles=plan.n_split_tiles, n_slots=plan.n_slots, chunk_tiles=plan.chunk)
+    dense = _lib.DenseArgs(
+        b=b_t.data_ptr(), ldb=ldb, b_col_major=int(col_major), N=N, b_scale=float(b_scale),
+        b_scale_vec=b_scale_vec.data_ptr() if b_scale_vec is not None else None,
+        bias=bias.data_ptr() if bias is not None else None,
+        c=target.data_ptr(), ldc=target.stride(0), out_dtype=_OUT_CODES[target.dtype],
+        activation=activation)
+    desc = dbsr.desc()
+    stream = torch.cuda.current_stream(out.device).cuda_stream
+    ws_ptr = ws.data_ptr() if ws is not None else None
+    if kind == "int8":
+        st = lib.void_spmm_int8(ctypes.byref(desc), ctypes.byref(dense), epilogue, ctypes.byref(cplan),
+                                ws_ptr, ws_bytes, stream)
+    else:
+        st = lib.void_spmm_fp8(ctypes.byref(desc), ctypes.byref(dense), ctypes.byref(cplan),
+                               ws_ptr, ws_bytes, stream)
+    _lib.check(st, f"void_spmm_{kind}")
+    if target is not out:
+        out.copy_(target)
+    return out
+
+
+def out_code(dtype: torch.dtype) -> int:
+    if dtype not in _OUT_CODES:
+        raise ValueError(f"unsupported output dtype {dtype}")
+    return _OUT_CODES[dtype]

@@ -1,0 +1,62 @@
+"""Build recipe for libvoid_amd.so (gfx950 HIP kernels + C ABI).
+
+Run ``python -m void_amd.build`` (or ``__graft_entry__.build()``).  The
+library is built in-tree next to this file so that it travels with the
+repository snapshot; nothing is installed.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO_DIR = PKG_DIR.parent
+SRC_DIR = PKG_DIR / "csrc"
+INCLUDE_DIR = REPO_DIR / "include"
+LIB_PATH = PKG_DIR / "libvoid_amd.so"
+ARCH = "gfx950"
+
+SOURCES = [SRC_DIR / "void_spmm.hip"]
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-shared",
+    "-fPIC",
+    # Exact control of rounding: every fused multiply-add in the kernels is
+    # an explicit fmaf, so the ROW_MEAN epilogue keeps separate mul / add.
+    "-ffp-contract=off",
+    # Packed fp32 VALU forms are kept out of generated code on this pool.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found; the gfx950 library cannot be built")
+    return path
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source into ``void_amd/libvoid_amd.so``."""
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", *map(str, SOURCES), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,264 @@
+"""FP8 (E4M3 / E5M2) quantisation of VOID tensors and the FP8 block-sparse SpMM.
+
+Mirrors ``void/fp8.py``: FP8Config / FP8ScalingInfo with the amax-history
+scaling rule, quantize_to_fp8 / dequantize_from_fp8, FP8VOIDTensor and
+void_spmm_fp8.  The reference kernel upcasts the FP8 tiles to fp32 and runs
+an fp32 (TF32) dot (fp8.py:577-671); here an E4M3 B operand feeds gfx950's
+fp8 x fp8 MFMA with fp32 accumulation directly, and per-tile scales are
+applied to each tile's fp32 partial product in registers.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from enum import Enum
+from typing import Dict, Literal, Optional, Tuple, Union
+
+import torch
+
+from . import _lib, _runtime, tuning
+
+
+class FP8Format(Enum):
+    E4M3 = "e4m3"
+    E5M2 = "e5m2"
+
+
+FP8_MAX = {FP8Format.E4M3: 448.0, FP8Format.E5M2: 57344.0}
+FP8_MIN = {FP8Format.E4M3: -448.0, FP8Format.E5M2: -57344.0}
+
+
+@dataclass
+class FP8Config:
+    """fp8.py:37-66."""
+    format: FP8Format = FP8Format.E4M3
+    scale_mode: Literal["per_tensor", "per_block", "per_row"] = "per_tensor"
+    margin: float = 0.0
+    amax_history_len: int = 16
+
+    @property
+    def max_value(self) -> float:
+        return FP8_MAX[self.format]
+
+    @property
+    def torch_dtype(self) -> torch.dtype:
+        return torch.float8_e4m3fn if self.format == FP8Format.E4M3 else torch.float8_e5m2
+
+
+@dataclass
+class FP8ScalingInfo:
+    """Scale, inverse scale and amax history (fp8.py:69-105)."""
+    scale: torch.Tensor
+    scale_inv: torch.Tensor
+    amax: torch.Tensor
+    amax_history: torch.Tensor
+    config: FP8Config = field(default_factory=FP8Config)
+
+    def update_amax(self, new_amax: torch.Tensor) -> None:
+        self.amax_history = torch.roll(self.amax_history, shifts=1, dims=-1)
+        if self.amax_history.dim() == 1:
+            self.amax_history[0] = new_amax
+        else:
+            self.amax_history[..., 0] = new_amax
+        self.amax = new_amax
+
+    def compute_scale(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        if self.amax_history.dim() == 1:
+            smoothed = self.amax_history.max()
+        else:
+            smoothed = self.amax_history.max(dim=-1).values
+        fp8_max = self.config.max_value * (1.0 - self.config.margin)
+        self.scale = torch.clamp(smoothed / fp8_max, min=1e-12)
+        self.scale_inv = 1.0 / self.scale
+        return self.scale, self.scale_inv
+
+
+def create_scaling_info(shape: Tuple[int, ...], config: FP8Config,
+                        device: Union[str, torch.device] = "cuda") -> FP8ScalingInfo:
+    """fp8.py:108-152."""
+    if config.scale_mode == "per_tensor":
+        scale_shape: Tuple[int, ...] = ()
+    elif config.scale_mode in ("per_block", "per_row"):
+        scale_shape = (shape[0],)
+    else:
+        raise ValueError(f"Unknown scale_mode: {config.scale_mode}")
+    hist = (config.amax_history_len,) if scale_shape == () else scale_shape + (config.amax_history_len,)
+    return FP8ScalingInfo(
+        scale=torch.ones(scale_shape, dtype=torch.float32, device=device),
+        scale_inv=torch.ones(scale_shape, dtype=torch.float32, device=device),
+        amax=torch.zeros(scale_shape, dtype=torch.float32, device=device),
+        amax_history=torch.zeros(hist, dtype=torch.float32, device=device),
+        config=config)
+
+
+def compute_amax(tensor: torch.Tensor, scale_mode: str = "per_tensor") -> torch.Tensor:
+    """fp8.py:159-182."""
+    if scale_mode == "per_tensor":
+        return tensor.abs().max()
+    if scale_mode in ("per_block", "per_row"):
+        return tensor.view(tensor.shape[0], -1).abs().max(dim=1).values
+    raise ValueError(f"Unknown scale_mode: {scale_mode}")
+
+
+def quantize_to_fp8(tensor: torch.Tensor, config: Optional[FP8Config] = None,
+                    scaling_info: Optional[FP8ScalingInfo] = None) -> Tuple[torch.Tensor, FP8ScalingInfo]:
+    """clamp(x * scale_inv, +-max).to(fp8) with amax-history scaling (fp8.py:185-229)."""
+    config = config or FP8Config()
+    if scaling_info is None:
+        scaling_info = create_scaling_info(tensor.shape, config, tensor.device)
+    scaling_info.update_amax(compute_amax(tensor, config.scale_mode))
+    _, scale_inv = scaling_info.compute_scale()
+    if config.scale_mode == "per_tensor":
+        scaled = tensor * scale_inv
+    else:
+        scaled = tensor * scale_inv.view((tensor.shape[0],) + (1,) * (tensor.dim() - 1))
+    scaled = torch.clamp(scaled, -config.max_value, config.max_value)
+    return scaled.to(config.torch_dtype), scaling_info
+
+
+def dequantize_from_fp8(tensor: torch.Tensor, scaling_info: FP8ScalingInfo,
+                        output_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """fp32(x) * scale (fp8.py:232-257)."""
+    f = tensor.to(torch.float32)
+    if scaling_info.config.scale_mode == "per_tensor":
+        r = f * scaling_info.scale
+    else:
+        r = f * scaling_info.scale.view((tensor.shape[0],) + (1,) * (tensor.dim() - 1))
+    return r.to(output_dtype)
+
+
+@dataclass
+class FP8VOIDTensor:
+    """VOID tensor with FP8 tiles (fp8.py:438-570)."""
+    values_fp8: torch.Tensor
+    scaling_info: FP8ScalingInfo
+    block_rows: torch.Tensor
+    block_cols: torch.Tensor
+    morton_codes: torch.Tensor
+    shape: Tuple[int, int]
+    tile_size: Tuple[int, int]
+    nnz_original: int
+    n_blocks: int
+    density: float
+    _device_bsr: Dict[str, "_runtime.DeviceBsr"] = field(default_factory=dict, repr=False)
+
+    @classmethod
+    def from_void_tensor(cls, void_tensor, config: Optional[FP8Config] = None) -> "FP8VOIDTensor":
+        config = config or FP8Config(scale_mode="per_block")
+        values_fp8, info = quantize_to_fp8(void_tensor.values, config=config)
+        return cls(values_fp8=values_fp8, scaling_info=info, block_rows=void_tensor.block_rows,
+                   block_cols=void_tensor.block_cols, morton_codes=void_tensor.morton_codes,
+                   shape=void_tensor.shape, tile_size=void_tensor.tile_size,
+                   nnz_original=void_tensor.nnz_original, n_blocks=void_tensor.n_blocks,
+                   density=void_tensor.density)
+
+    def to_void_tensor(self, output_dtype: torch.dtype = torch.float16):
+        from .format import VOIDTensor
+        values = dequantize_from_fp8(self.values_fp8, self.scaling_info, output_dtype=output_dtype)
+        return VOIDTensor(values=values, block_rows=self.block_rows, block_cols=self.block_cols,
+                          morton_codes=self.morton_codes, shape=self.shape, tile_size=self.tile_size,
+                          nnz_original=self.nnz_original, n_blocks=self.n_blocks, density=self.density,
+                          dtype=output_dtype)
+
+    def to(self, device: Union[str, torch.device]) -> "FP8VOIDTensor":
+        si = self.scaling_info
+        return FP8VOIDTensor(
+            values_fp8=self.values_fp8.to(device),
+            scaling_info=FP8ScalingInfo(scale=si.scale.to(device), scale_inv=si.scale_inv.to(device),
+                                        amax=si.amax.to(device), amax_history=si.amax_history.to(device),
+                                        config=si.config),
+            block_rows=self.block_rows.to(device), block_cols=self.block_cols.to(device),
+            morton_codes=self.morton_codes.to(device), shape=self.shape, tile_size=self.tile_size,
+            nnz_original=self.nnz_original, n_blocks=self.n_blocks, density=self.density)
+
+    def cuda(self) -> "FP8VOIDTensor":
+        return self.to("cuda")
+
+    @property
+    def memory_bytes(self) -> int:
+        return (self.values_fp8.numel() + self.scaling_info.scale.numel() * 4
+                + (self.block_rows.numel() + self.block_cols.numel()) * 4)
+
+    def device_bsr(self) -> "_runtime.DeviceBsr":
+        key = str(self.values_fp8.device)
+        d = self._device_bsr.get(key)
+        if d is None:
+            if self.values_fp8.dtype != torch.float8_e4m3fn:
+                raise NotImplementedError(f"the FP8 kernel takes E4M3FN tiles, got {self.values_fp8.dtype}")
+            per_tensor = self.scaling_info.config.scale_mode == "per_tensor"
+            scales = self.scaling_info.scale.reshape(-1)
+            d = _runtime.make_device_bsr(self.values_fp8, scales, self.block_rows, self.block_cols,
+                                         self.shape, self.tile_size, self.values_fp8.device, per_tensor)
+            self._device_bsr[key] = d
+        return d
+
+    def __repr__(self) -> str:
+        return (f"FP8VOIDTensor(shape={self.shape}, tile_size={self.tile_size}, n_blocks={self.n_blocks}, "
+                f"format={self.scaling_info.config.format.value}, "
+                f"scale_mode={self.scaling_info.config.scale_mode})")
+
+
+def quantize_dense_fp8(b: torch.Tensor) -> Tuple[torch.Tensor, float]:
+    """Per-tensor E4M3 quantisation of a dense operand: (fp8 tensor, scale)."""
+    q, info = quantize_to_fp8(b.float(), FP8Config(scale_mode="per_tensor"))
+    return q, float(info.scale.item())
+
+
+def void_spmm_fp8(a: FP8VOIDTensor, b: torch.Tensor, output_dtype: torch.dtype = torch.float16, *,
+                  b_scale: Optional[Union[float, torch.Tensor]] = None, activation: str = "none",
+                  bias: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                  chunk_tiles: Optional[int] = None) -> torch.Tensor:
+    """FP8 block-sparse SpMM C = A @ B (fp8.py:674-742) on the gfx950 fp8 MFMA kernel.
+
+    B in float8_e4m3fn is used as given, multiplied by b_scale (default 1.0;
+    a scalar or N per-column scales).  A float B is first quantised per
+    tensor to E4M3 (its amax / 448 scale) — the reference instead keeps B
+    in fp32 for its TF32 dot, so this path carries B's quantisation error as
+    well.  Output dtype float32 / bfloat16 / float16.
+    """
+    assert b.dim() == 2
+    assert a.shape[1] == b.shape[0]
+    _runtime.require_gpu(b, "B")
+    M, K = a.shape
+    N = b.shape[1]
+    if b.dtype != torch.float8_e4m3fn:
+        if b.dtype == torch.float8_e5m2:
+            raise NotImplementedError("E5M2 B operands are not supported by the gfx950 kernel")
+        b, s = quantize_dense_fp8(b)
+        if b_scale is not None:
+            raise ValueError("b_scale is only meaningful for an already-quantised float8 B")
+        b_scale = s
+    from .int_quant import _b_scale_args
+    scalar_scale, scale_vec = _b_scale_args(b_scale, N, b.device)
+    if out is None:
+        out = torch.empty(M, N, dtype=output_dtype, device=b.device)
+    elif out.shape != (M, N) or out.dtype != output_dtype:
+        raise ValueError(f"out must be [{M}, {N}] {output_dtype}")
+    if a.n_blocks == 0:
+        out.zero_()
+        if bias is not None or activation != "none":
+            from .fusion import apply_activation_torch
+            out.copy_(apply_activation_torch(out.float() + (bias if bias is not None else 0), activation))
+        return out
+    _runtime.require_gpu(a.values_fp8, "A")
+    from .fusion import get_activation_code
+    if bias is not None:
+        bias = bias.to(device=b.device, dtype=torch.float32).contiguous()
+    chunk = chunk_tiles or tuning.select_chunk("fp8", a.n_blocks, N)
+    return _runtime.launch("fp8", a.device_bsr(), b.view(torch.uint8) if b.dim() == 2 else b,
+                           b_scale=scalar_scale, b_scale_vec=scale_vec, out=out,
+                           epilogue=_lib.EPI_PER_BLOCK, activation=get_activation_code(activation),
+                           bias=bias, chunk=chunk)
+
+
+def void_tensor_to_fp8(void_tensor, format: str = "e4m3", scale_mode: str = "per_block") -> FP8VOIDTensor:
+    """fp8.py:749-766."""
+    fmt = FP8Format.E4M3 if format == "e4m3" else FP8Format.E5M2
+    return FP8VOIDTensor.from_void_tensor(void_tensor, FP8Config(format=fmt, scale_mode=scale_mode))
+
+
+__all__ = [
+    "FP8Format", "FP8_MAX", "FP8_MIN", "FP8Config", "FP8ScalingInfo", "FP8VOIDTensor",
+    "create_scaling_info", "compute_amax", "quantize_to_fp8", "dequantize_from_fp8",
+    "quantize_dense_fp8", "void_spmm_fp8", "void_tensor_to_fp8",
+]

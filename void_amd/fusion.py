@@ -1,0 +1,113 @@
+"""Fused SpMM + activation on quantised VOID tensors.
+
+Mirrors the activation helpers and ``void_spmm_gelu`` / ``void_spmm_relu`` /
+``void_spmm_silu`` of ``void/fusion.py``.  The reference fuses bias and
+activation into its fp32 SpMM kernel (void_spmm_activation_kernel,
+fusion.py:98-198); here the same epilogue (``+ bias[n]``, then the
+activation, then the cast to the output dtype) runs in registers at the end
+of the INT8 or FP8 gfx950 kernel.  GELU is the tanh form of fusion.py:38-43.
+"""
+
+from __future__ import annotations
+
+from enum import Enum
+from typing import Optional, Union
+
+import torch
+
+
+class ActivationType(Enum):
+    """fusion.py:24-31."""
+    NONE = "none"
+    RELU = "relu"
+    GELU = "gelu"
+    SILU = "silu"
+    TANH = "tanh"
+    SIGMOID = "sigmoid"
+
+
+_CODES = {"none": 0, "relu": 1, "gelu": 2, "silu": 3, "swish": 3, "tanh": 4, "sigmoid": 5}
+
+
+def get_activation_code(activation: Union[str, ActivationType]) -> int:
+    """Activation name -> kernel code (fusion.py:77-91); unknown names map to 0.
+
+    Codes 4 (tanh) and 5 (sigmoid) exist in the reference's table but not in
+    the gfx950 epilogue, which raises for them.
+    """
+    if isinstance(activation, ActivationType):
+        activation = activation.value
+    code = _CODES.get(str(activation).lower(), 0)
+    if code > 3:
+        raise NotImplementedError(f"activation {activation!r} is not fused by the gfx950 kernel")
+    return code
+
+
+def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
+    """tanh-form GELU exactly as written in fusion.py:38-43."""
+    inner = 0.7978845608 * (x + 0.044715 * x * x * x)
+    return x * 0.5 * (1.0 + (2.0 * torch.sigmoid(2.0 * inner) - 1.0))
+
+
+def apply_activation_torch(x: torch.Tensor, activation: str) -> torch.Tensor:
+    """Activation of an all-empty matrix (no tiles): the reference's own torch
+    calls for that case (fusion.py:466-476; GELU there is torch's erf form)."""
+    if activation == "relu":
+        return torch.relu(x)
+    if activation == "gelu":
+        return torch.nn.functional.gelu(x)
+    if activation in ("silu", "swish"):
+        return torch.nn.functional.silu(x)
+    return x
+
+
+def _spmm_activation(a, b: torch.Tensor, bias: Optional[torch.Tensor], out: Optional[torch.Tensor],
+                     activation: str, b_scale=None, out_dtype: Optional[torch.dtype] = None,
+                     epilogue: Optional[str] = None) -> torch.Tensor:
+    from .fp8 import FP8VOIDTensor, void_spmm_fp8
+    from .int_quant import Int8VOIDTensor, void_spmm_int8
+    if out_dtype is None:
+        out_dtype = out.dtype if out is not None else (b.dtype if b.is_floating_point()
+                                                       and b.dtype in (torch.float32, torch.bfloat16,
+                                                                       torch.float16) else torch.float32)
+    if isinstance(a, Int8VOIDTensor):
+        if epilogue is None and b.dtype == torch.int8 and b_scale is not None:
+            epilogue = "per_block"
+        return void_spmm_int8(a, b, b_scale=b_scale, out=out, epilogue=epilogue, out_dtype=out_dtype,
+                              activation=activation, bias=bias)
+    if isinstance(a, FP8VOIDTensor):
+        return void_spmm_fp8(a, b, output_dtype=out_dtype, b_scale=b_scale, activation=activation,
+                             bias=bias, out=out)
+    raise NotImplementedError(
+        "the gfx950 fused SpMM takes quantised tiles (Int8VOIDTensor or FP8VOIDTensor); quantise the "
+        "VOIDTensor with quantize_void_tensor or void_tensor_to_fp8 first")
+
+
+def void_spmm_gelu(a, b: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                   out: Optional[torch.Tensor] = None, *, b_scale=None,
+                   out_dtype: Optional[torch.dtype] = None, epilogue: Optional[str] = None) -> torch.Tensor:
+    """C = GELU(A @ B + bias) (fusion.py:381-399) with a quantised A.
+
+    Int8VOIDTensor A: float B is quantised per tensor as void_spmm_int8
+    does; an int8 B with b_scale (scalar or per column) uses the per-block
+    epilogue (true dequantisation) unless ``epilogue`` says otherwise.
+    Output dtype: ``out_dtype``, else out's dtype, else B's float dtype,
+    else float32.
+    """
+    return _spmm_activation(a, b, bias, out, "gelu", b_scale, out_dtype, epilogue)
+
+
+def void_spmm_relu(a, b: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                   out: Optional[torch.Tensor] = None, **kw) -> torch.Tensor:
+    """C = ReLU(A @ B + bias) (fusion.py:402-420)."""
+    return _spmm_activation(a, b, bias, out, "relu", kw.get("b_scale"), kw.get("out_dtype"), kw.get("epilogue"))
+
+
+def void_spmm_silu(a, b: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                   out: Optional[torch.Tensor] = None, **kw) -> torch.Tensor:
+    """C = SiLU(A @ B + bias) (fusion.py:423-441)."""
+    return _spmm_activation(a, b, bias, out, "silu", kw.get("b_scale"), kw.get("out_dtype"), kw.get("epilogue"))
+
+
+__all__ = ["ActivationType", "get_activation_code", "gelu_tanh", "void_spmm_gelu", "void_spmm_relu",
+           "void_spmm_silu"]

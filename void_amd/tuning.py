@@ -1,0 +1,47 @@
+"""Fixed gfx950 launch configuration (replaces the reference's autotuner).
+
+The reference searches TILE_N x num_warps x num_stages at run time and keeps
+a JSON cache (void/autotune.py:39-104, 345-381).  On MI355X the kernel shape
+is fixed by the hardware instead:
+
+* one workgroup = 4 wave64s, one 32-row block-row x 128-column panel of C,
+  64 KB of LDS for the cross-wave reduction -> 2 workgroups per CU;
+* 256 CUs in 8 XCDs -> 512 resident workgroups;
+* the only shape-dependent knob is the Stream-K chunk: the most tiles one
+  work item may take before its block-row is split.  It is the larger of a
+  floor (splitting costs a partial-tile round trip through L2) and the
+  average work per resident workgroup, so that no item is longer than the
+  average load of a workgroup slot.
+"""
+
+from __future__ import annotations
+
+import math
+
+GFX950_CUS = 256
+GFX950_XCDS = 8
+WAVES_PER_WORKGROUP = 4
+WORKGROUPS_PER_CU = 2
+PANEL_COLUMNS = 128
+TILE = 32
+
+# (name, floor on the chunk, factor on the per-slot average)
+CHUNK_TABLE = {
+    "int8": (16, 1.0),
+    "fp8": (16, 1.0),
+}
+
+
+def resident_workgroups() -> int:
+    return GFX950_CUS * WORKGROUPS_PER_CU
+
+
+def n_panels(N: int) -> int:
+    return (N + PANEL_COLUMNS - 1) // PANEL_COLUMNS
+
+
+def select_chunk(kind: str, n_blocks: int, N: int) -> int:
+    """Stream-K chunk (max tiles per work item) for a problem."""
+    floor, factor = CHUNK_TABLE[kind]
+    per_slot = n_blocks * n_panels(max(N, 1)) / resident_workgroups()
+    return max(floor, int(math.ceil(per_slot * factor)))
