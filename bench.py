@@ -1,0 +1,264 @@
+"""Benchmark of the quantised block-sparse SpMM on one MI355X.
+
+Default workload: A 4096x4096 in 32x32 tiles at
+90 % block sparsity (1638 uniformly chosen tiles, N(0,1) entries, INT8
+per-tile), B 4096x512 N(0,1) INT8 per-column, fp32 output, per-block
+dequantising epilogue.  One "step" is one SpMM launch over that batch with
+all inputs resident in HBM.
+
+Timing: the K steps are captured in a HIP graph, each step preceded by an
+overwrite of a 1 GiB buffer so that L2 and the 256 MB Infinity Cache hold
+none of the inputs (cold cache); the graph replay is bracketed by HIP events
+on the launch stream, and the replay time of a graph of the overwrites
+alone is subtracted.  A hot-cache figure (a graph of back-to-back launches)
+is reported alongside.
+
+value = effective TOPS = 2 * n_tiles * 32 * 32 * N / kernel time (nonzero
+tiles only).  roofline: HBM-bound; achieved = algorithmic bytes (A tiles +
+A scales + column indices + row pointer + B + B scales + C, each once) /
+kernel time, against 8 TB/s.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0   # dense MFMA int8, MI355X
+FP8_PEAK_TFLOPS = 5000.0  # dense MFMA fp8, MI355X
+
+# Per-launch HBM traffic of the dominant kernel measured with rocprofv3 --pmc
+# (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration); None
+# until measured for a workload.
+MEASURED_TRAFFIC = {}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--epilogue", default=None, help="int8 epilogue (default per_block)")
+    ap.add_argument("--chunk", type=int, default=None, help="override the Stream-K chunk")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
+    ap.add_argument("--profile", action="store_true", help="no CPU leg, no flush: for rocprofv3 runs")
+    return ap.parse_args()
+
+
+def build_problem(cfg: str, dev, epilogue):
+    import torch
+
+    import cases
+    import oracle
+    import void_amd
+
+    if cfg == "c1":
+        A, B = cases.c1_plumbing()
+        vt = void_amd.csr_to_void(A)
+        case = cases.BlockCase("c1_plumbing_512_n128", 512, 512, 128, vt.values.numpy(),
+                               vt.block_rows.numpy(), vt.block_cols.numpy(), B)
+    else:
+        case = {"c2": cases.c2_int8, "c3": cases.c3_fp8, "c4": cases.c4_powerlaw, "c5": cases.c5_ffn}[cfg]()
+        vt = cases.make_void_tensor(case, "cpu")
+    M, K, N = case.M, case.K, case.N
+    nb = len(case.block_rows)
+    nbr = -(-M // 32)
+    prob = {"case": case, "M": M, "K": K, "N": N, "nb": nb}
+    if cfg == "c3":
+        f8 = void_amd.void_tensor_to_fp8(vt).to(dev)
+        bq, bs = oracle.quantize_fp8_tensor(case.b)
+        bt = torch.from_numpy(bq).to(dev).view(torch.float8_e4m3fn)
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+
+        def run():
+            return void_amd.void_spmm_fp8(f8, bt, output_dtype=torch.bfloat16, b_scale=float(bs), out=out)
+
+        prob.update(kind="fp8", dtype="fp8e4m3", out_bytes=2, b_scale_bytes=0, run=run,
+                    peak_ops=FP8_PEAK_TFLOPS, epilogue="per_block")
+        a_scales = f8.scaling_info.scale.cpu().numpy()
+        tiles_f = f8.values_fp8.float().cpu()
+        b_deq = torch.from_numpy(oracle.e4m3_table()[bq.astype(np.int64)].astype(np.float32) * bs)
+    else:
+        q = void_amd.quantize_void_tensor(vt)
+        qd = q.to(dev)
+        if cfg == "c1":
+            bq, bs = oracle.quantize_i8_tensor(case.b)
+            st = float(bs)
+            bsv = np.full(N, bs, np.float32)
+        else:
+            bq, bsv = oracle.quantize_i8_columns(case.b)
+            st = torch.from_numpy(bsv).to(dev)
+        bt = torch.from_numpy(bq).to(dev)
+        gelu = cfg == "c5"
+        ep = epilogue or ("row_mean" if cfg == "c1" else "per_block")
+        out_dtype = torch.bfloat16 if gelu else torch.float32
+        out = torch.empty(M, N, dtype=out_dtype, device=dev)
+        def run():
+            if gelu:
+                return void_amd.void_spmm_gelu(qd, bt, b_scale=st, out=out, out_dtype=torch.bfloat16,
+                                               epilogue=ep)
+            return void_amd.void_spmm_int8(qd, bt, b_scale=st, out=out, epilogue=ep, chunk_tiles=prob.get("chunk"))
+
+        prob.update(kind="int8", dtype="int8", out_bytes=2 if gelu else 4,
+                    b_scale_bytes=0 if cfg == "c1" else 4 * N, run=run, peak_ops=INT8_PEAK_TOPS,
+                    epilogue=ep, qd=qd)
+        a_scales = q.scales.cpu().numpy()
+        tiles_f = q.values.float()
+        b_deq = torch.from_numpy(bq.astype(np.float32) * bsv[None, :])
+    prob["ops"] = 2.0 * nb * 32 * 32 * N
+    a_elem = 1
+    prob["bytes"] = (nb * 1024 * a_elem + 4 * nb + 4 * nb + 4 * (nbr + 1) + K * N * 1
+                     + prob["b_scale_bytes"] + M * N * prob["out_bytes"])
+    prob["cpu"] = dict(tiles=tiles_f, scales=torch.from_numpy(np.asarray(a_scales, np.float32).reshape(-1)),
+                       col_idx=torch.from_numpy(case.block_cols.astype(np.int64)),
+                       row=torch.from_numpy(case.block_rows.astype(np.int64)), b=b_deq)
+    return prob
+
+
+def time_gpu(prob, steps: int, warmup: int, flush: bool):
+    """Kernel time from HIP-graph replays, so host launch overhead is excluded.
+
+    cold: a graph of `steps` x (overwrite a 1 GiB buffer, SpMM) minus a graph of
+    `steps` x (overwrite) -- the SpMM then always starts with L2 and the
+    Infinity Cache holding none of its inputs; hot: a graph of `steps` x SpMM.
+    Both graphs are bracketed by events on the capture-replay stream with a
+    device synchronisation on either side.
+    """
+    import torch
+    run = prob["run"]
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    scratch = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+
+    def capture(body):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(steps):
+                body(i)
+        return g
+
+    def replay_ms(g, reps=3):
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    def cold_body(i):
+        scratch.fill_(float(i))
+        run()
+
+    t0 = time.perf_counter()
+    g_hot = capture(lambda i: run())
+    hot = replay_ms(g_hot) / steps
+    cold = None
+    if flush:
+        g_cold = capture(cold_body)
+        g_flush = capture(lambda i: scratch.fill_(float(i)))
+        cold = (replay_ms(g_cold) - replay_ms(g_flush)) / steps
+    wall = time.perf_counter() - t0
+    return cold, hot, wall
+
+
+def time_cpu(prob, budget_s: float):
+    import torch
+
+    import oracle
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    c = prob["cpu"]
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while True:
+        t = time.perf_counter()
+        oracle.cpu_baseline_spmm(c["tiles"], c["scales"], c["col_idx"], c["row"], c["b"], prob["M"])
+        times.append(time.perf_counter() - t)
+        if time.perf_counter() > t_end and len(times) >= 3:
+            break
+    med = statistics.median(times[1:]) if len(times) > 1 else times[0]
+    return med, threads, len(times)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); every GPU box here has one "
+              "GPU and the SpMM path is built and measured on a single MI355X.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    prob = build_problem(args.config, dev, args.epilogue)
+    if args.chunk:
+        prob["chunk"] = args.chunk
+    cold, hot, wall = time_gpu(prob, args.steps, args.warmup, flush=not args.profile)
+    t_ms = cold if cold is not None else hot
+    tops = prob["ops"] / (t_ms * 1e-3) / 1e12
+    gbs = prob["bytes"] / (t_ms * 1e-3) / 1e9
+    t_roof_mem = prob["bytes"] / (HBM_PEAK_GBS * 1e9)
+    t_roof_ops = prob["ops"] / (prob["peak_ops"] * 1e12)
+    bound = "hbm" if t_roof_mem >= t_roof_ops else "mfma"
+    if bound == "hbm":
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    else:
+        roof = {"bound": "mfma", "achieved": round(tops, 2), "peak": prob["peak_ops"], "unit": "TFLOP/s",
+                "frac": round(tops / prob["peak_ops"], 4)}
+    roof["traffic"] = MEASURED_TRAFFIC.get(args.config)
+    roof["algorithmic_bytes"] = prob["bytes"]
+    cpu = None
+    if args.cpu_seconds > 0 and not args.profile:
+        med, threads, reps = time_cpu(prob, args.cpu_seconds)
+        cpu = {"value": round(prob["ops"] / med / 1e12, 4), "unit": "TOPS", "cores": threads, "kind": "port",
+               "ms": round(med * 1e3, 3),
+               "sample": f"full {args.config} problem, torch CPU dequantise + tile bmm + index_add, "
+                         f"median of {reps - 1} reps after 1 warm-up"}
+    case = prob["case"]
+    line = {
+        "metric": "INT8 BSpMM effective TOPS + % roofline, 4096x4096 90% sparse, N=512",
+        "value": round(tops, 3),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": prob["dtype"],
+        "data": "synthetic (seeded generators of BASELINE.json configs)",
+        "config": {"workload": case.name, "M": prob["M"], "K": prob["K"], "N": prob["N"],
+                   "n_tiles": prob["nb"], "epilogue": prob["epilogue"], "kind": prob["kind"],
+                   "cache": "cold (1 GiB overwrite between steps)" if not args.profile else "hot"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "extra": {"hot_ms": round(hot, 5),
+                  "hot_tops": round(prob["ops"] / (hot * 1e-3) / 1e12, 3),
+                  "hot_gbs": round(prob["bytes"] / (hot * 1e-3) / 1e9, 1),
+                  "roofline_ms": round(max(t_roof_mem, t_roof_ops) * 1e3, 5),
+                  "dense_equiv_tops": round(2.0 * prob["M"] * prob["K"] * prob["N"] / (t_ms * 1e-3) / 1e12, 2),
+                  "wall_s": round(wall, 3)},
+    }
+    if args.config != "c2":
+        line["metric"] = f"{prob['kind'].upper()} BSpMM effective TOPS + % roofline, {case.name}"
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

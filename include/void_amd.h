@@ -81,15 +81,21 @@ typedef struct void_bsr_desc {
   int32_t reserved;
 } void_bsr_desc;
 
+#define VOID_ITEM_INLINE_COLS 24
+
 /* One unit of work: tiles [begin, end) of block-row `row`.  A row with more
  * tiles than the plan's chunk size is split into `nchunks` items that each
  * write a partial tile into workspace slot (slot + chunk); the last of them
  * to finish (counted on split tile `tile`) reduces the partials in chunk
  * order and applies the epilogue.  tile == -1 marks an unsplit row.
+ * cols[] repeats the block columns of the item's first 24 tiles so that a
+ * workgroup reads its first B addresses together with the item (128 bytes,
+ * one scalar load burst) instead of after it.
  * Replaces StreamKWorkload (void/stream_k.py:13-33). */
 typedef struct void_work_item {
   int32_t row, begin, end, tile;
   int32_t nchunks, chunk, slot, reserved;
+  int32_t cols[VOID_ITEM_INLINE_COLS];
 } void_work_item;
 
 /* A plan from void_streamk_plan with its items copied to device memory. */
@@ -132,11 +138,12 @@ int void_panel_width(void);
  * with more than chunk_tiles tiles, which are split into ceil(n/chunk_tiles)
  * near-equal chunks.  Items are ordered longest-first; empty rows are kept
  * (they produce the zero / activation(bias) rows of C).
- * row_ptr is a HOST array of n_block_rows + 1 entries.
+ * row_ptr (n_block_rows + 1 entries) and col_idx (row_ptr[n_block_rows]
+ * entries, or NULL to leave cols[] at -1) are HOST arrays.
  * On VOID_ERR_CAPACITY, *n_items holds the required capacity. */
-int void_streamk_plan(const int32_t* row_ptr, int32_t n_block_rows, int32_t chunk_tiles,
-                      void_work_item* items, int32_t capacity, int32_t* n_items,
-                      int32_t* n_split_tiles, int32_t* n_slots);
+int void_streamk_plan(const int32_t* row_ptr, const int32_t* col_idx, int32_t n_block_rows,
+                      int32_t chunk_tiles, void_work_item* items, int32_t capacity,
+                      int32_t* n_items, int32_t* n_split_tiles, int32_t* n_slots);
 
 /* Bytes of device workspace a plan needs for N output columns (0 if the plan
  * splits no row).  The first n_split_tiles * n_panels int32 counters of the

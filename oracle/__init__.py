@@ -296,9 +296,13 @@ def cpu_baseline_spmm(tiles_f32, scales, col_idx, row_of_tile, b_deq, M: int):
     """
     import torch
     K, N = b_deq.shape
-    a_deq = tiles_f32 * scales[:, None, None]
-    panels = b_deq.view(K // TILE, TILE, N)[col_idx]
-    prod = torch.bmm(a_deq, panels)
+    kb = -(-K // TILE)
+    if K % TILE:
+        b_deq = torch.nn.functional.pad(b_deq, (0, 0, 0, kb * TILE - K))
     out = torch.zeros(-(-M // TILE), TILE, N, dtype=torch.float32)
-    out.index_add_(0, row_of_tile, prod)
+    step = max(1, (1 << 26) // (TILE * max(N, 1)))  # bound the gathered B panels to 256 MB
+    for s in range(0, tiles_f32.shape[0], step):
+        a_deq = tiles_f32[s:s + step] * scales[s:s + step, None, None]
+        panels = b_deq.view(kb, TILE, N)[col_idx[s:s + step]]
+        out.index_add_(0, row_of_tile[s:s + step], torch.bmm(a_deq, panels))
     return out.view(-1, N)[:M]

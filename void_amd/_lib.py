@@ -52,9 +52,14 @@ class BsrDesc(ctypes.Structure):
     ]
 
 
+ITEM_INLINE_COLS = 24
+ITEM_INTS = 8 + ITEM_INLINE_COLS
+
+
 class WorkItem(ctypes.Structure):
     _fields_ = [(name, c_int32) for name in
-                ("row", "begin", "end", "tile", "nchunks", "chunk", "slot", "reserved")]
+                ("row", "begin", "end", "tile", "nchunks", "chunk", "slot", "reserved")] + [
+                    ("cols", c_int32 * ITEM_INLINE_COLS)]
 
 
 class Plan(ctypes.Structure):
@@ -88,8 +93,9 @@ SIGNATURES = {
     "void_abi_version": (c_int, []),
     "void_last_error": (c_char_p, []),
     "void_panel_width": (c_int, []),
-    "void_streamk_plan": (c_int, [POINTER(c_int32), c_int32, c_int32, POINTER(WorkItem), c_int32,
-                                  POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
+    "void_streamk_plan": (c_int, [POINTER(c_int32), POINTER(c_int32), c_int32, c_int32,
+                                  POINTER(WorkItem), c_int32, POINTER(c_int32), POINTER(c_int32),
+                                  POINTER(c_int32)]),
     "void_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
     "void_spmm_int8": (c_int, [POINTER(BsrDesc), POINTER(DenseArgs), c_int32, POINTER(Plan),
                                c_void_p, c_size_t, c_void_p]),

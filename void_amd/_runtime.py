@@ -29,12 +29,12 @@ _OUT_CODES = {
 
 @dataclass
 class DevicePlan:
-    items: torch.Tensor          # int32 [n_items, 8] on device (void_work_item)
+    items: torch.Tensor          # int32 [n_items, 32] on device (void_work_item)
     n_items: int
     n_split_tiles: int
     n_slots: int
     chunk: int
-    host_items: np.ndarray       # int32 [n_items, 8] copy, for inspection
+    host_items: np.ndarray       # int32 [n_items, 32] copy, for inspection
     workspaces: Dict[int, torch.Tensor] = field(default_factory=dict)
 
     def workspace(self, N: int, device: torch.device) -> Tuple[Optional[torch.Tensor], int]:
@@ -49,10 +49,13 @@ class DevicePlan:
         return ws, nbytes
 
 
-def plan_rows(row_ptr_host: np.ndarray, chunk: int) -> Tuple[np.ndarray, int, int]:
-    """Run the C planner on a host row pointer; returns (items[n,8], n_split_tiles, n_slots)."""
+def plan_rows(row_ptr_host: np.ndarray, chunk: int,
+              col_idx_host: Optional[np.ndarray] = None) -> Tuple[np.ndarray, int, int]:
+    """Run the C planner on host index arrays; returns (items[n, 32] int32, n_split_tiles, n_slots)."""
     lib = _lib.lib()
     rp = np.ascontiguousarray(row_ptr_host, dtype=np.int32)
+    ci = None if col_idx_host is None else np.ascontiguousarray(col_idx_host, dtype=np.int32)
+    ci_ptr = None if ci is None else ci.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
     n_br = rp.size - 1
     n_items = ctypes.c_int32()
     n_tiles = ctypes.c_int32()
@@ -61,14 +64,15 @@ def plan_rows(row_ptr_host: np.ndarray, chunk: int) -> Tuple[np.ndarray, int, in
     cap = max(n_br, 1)
     while True:
         buf = (_lib.WorkItem * cap)()
-        st = lib.void_streamk_plan(rp_ptr, n_br, int(chunk), buf, cap, ctypes.byref(n_items),
+        st = lib.void_streamk_plan(rp_ptr, ci_ptr, n_br, int(chunk), buf, cap, ctypes.byref(n_items),
                                    ctypes.byref(n_tiles), ctypes.byref(n_slots))
         if st == -5 and n_items.value > cap:
             cap = n_items.value
             continue
         _lib.check(st, "void_streamk_plan")
         break
-    items = np.frombuffer(buf, dtype=np.int32, count=n_items.value * 8).reshape(n_items.value, 8).copy()
+    W = _lib.ITEM_INTS
+    items = np.frombuffer(buf, dtype=np.int32, count=n_items.value * W).reshape(n_items.value, W).copy()
     return items, n_tiles.value, n_slots.value
 
 
@@ -79,6 +83,7 @@ class DeviceBsr:
     row_ptr: torch.Tensor        # int32 [n_block_rows + 1]
     col_idx: torch.Tensor        # int32 [n_blocks]
     row_ptr_host: np.ndarray
+    col_idx_host: np.ndarray
     per_tensor: bool
     M: int
     K: int
@@ -89,7 +94,7 @@ class DeviceBsr:
     def plan(self, chunk: int) -> DevicePlan:
         p = self.plans.get(chunk)
         if p is None:
-            items, n_tiles, n_slots = plan_rows(self.row_ptr_host, chunk)
+            items, n_tiles, n_slots = plan_rows(self.row_ptr_host, chunk, self.col_idx_host)
             dev_items = torch.from_numpy(items).to(self.row_ptr.device)
             p = DevicePlan(dev_items, items.shape[0], n_tiles, n_slots, chunk, items)
             self.plans[chunk] = p
@@ -124,7 +129,8 @@ def make_device_bsr(values: torch.Tensor, scales: torch.Tensor, block_rows: torc
     else:
         s = s.index_select(0, lay.order).contiguous() if s.numel() else s.contiguous()
     return DeviceBsr(tiles=tiles, scales=s, row_ptr=lay.row_ptr, col_idx=lay.col_idx,
-                     row_ptr_host=lay.row_ptr_host, per_tensor=per_tensor, M=M, K=K,
+                     row_ptr_host=lay.row_ptr_host, col_idx_host=lay.col_idx.cpu().numpy(),
+                     per_tensor=per_tensor, M=M, K=K,
                      n_blocks=int(values.shape[0]), n_block_rows=n_br)
 
 

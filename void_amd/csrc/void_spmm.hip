@@ -14,11 +14,19 @@
 // the epilogue every lane owns four adjacent columns, so C is written with
 // full 16-byte stores.  A operand: lane (j, g) reads bytes [16g, 16g+16) of
 // tile row j, the same k set, so the k permutation agrees for A and B.
+// A column-major B (activations stored token-major) is loaded as 16 bytes
+// per column directly, with no transpose.
+//
+// Latency: the work item (128 bytes) carries the block columns of its first
+// 24 tiles, so the B addresses of the first batches come with the item; the
+// epilogue's scale, bias and row-mean factors are loaded before the tile
+// loop; each wave keeps the loads of kBatch tiles in flight.
 //
 // Cross-wave reduction goes through LDS (4 x 16 KB).  Rows that the planner
-// split into several items write partial tiles to a workspace; the last
-// chunk to arrive (agent-scope atomic counter) sums the partials in chunk
-// order and applies the epilogue, so results do not depend on timing.
+// split into several items write partial tiles to a workspace with
+// agent-coherent stores; the last chunk to arrive (agent-scope atomic
+// counter) sums the partials in chunk order and applies the epilogue, so
+// results do not depend on timing.
 
 #include <hip/hip_runtime.h>
 
@@ -27,6 +35,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 #include "void_amd.h"
@@ -40,6 +49,9 @@ constexpr int kWaves = 4;
 constexpr int kColsPerLane = 4;
 constexpr int kPanel = 32 * kColsPerLane;  // 128 output columns per workgroup
 constexpr int kThreads = 64 * kWaves;
+constexpr int kBatch = 5;                  // tiles whose loads one wave keeps in flight
+constexpr int kInline = VOID_ITEM_INLINE_COLS;
+constexpr int kRowsPerWave = kTile / kWaves;  // epilogue rows per wave
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -60,6 +72,7 @@ struct Params {
   const void_work_item* items;
   unsigned* counters;
   void* partials;
+  unsigned long long* trace;  // per-workgroup phase timestamps (instrumented builds only)
   int64_t ldb;
   int64_t ldc;
   float b_scale;
@@ -67,15 +80,63 @@ struct Params {
   int32_t M, N, K;
   int32_t n_panels;
   int32_t activation;
+  int32_t n_items;
+  int32_t panel_group;  // panels one XCD's share of the grid covers (see wg_tile)
 };
 
-// Workgroups are dispatched round-robin over the 8 XCDs.  Remap so that the
-// panels of one work item (consecutive logical ids) run on the same XCD and
-// share its L2 for the item's A tiles.
+#ifdef VOID_TRACE
+// Realtime stamps are kept in scalar registers and written once at exit, so
+// that nothing is stored before the kernel's loads (a store would stop the
+// compiler from using scalar loads for the read-only inputs).
+#define TRACE_DECL unsigned long long tr0 = 0, tr1 = 0, tr2 = 0, tr3 = 0, tr4 = 0, tr5 = 0, tr6 = 0
+#define TRACE_POINT(k) asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(tr##k))
+#define TRACE_FLUSH()                                                              \
+  do {                                                                             \
+    if (p.trace && threadIdx.x == 0) {                                             \
+      unsigned long long* t_ = p.trace + (size_t)blockIdx.x * 8;                   \
+      t_[0] = tr0; t_[1] = tr1; t_[2] = tr2; t_[3] = tr3;                          \
+      t_[4] = tr4; t_[5] = tr5; t_[6] = tr6;                                       \
+    }                                                                              \
+  } while (0)
+#else
+#define TRACE_DECL \
+  do {             \
+  } while (0)
+#define TRACE_POINT(k) \
+  do {                 \
+  } while (0)
+#define TRACE_FLUSH() \
+  do {                \
+  } while (0)
+#endif
+
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own
+// L2.  xcd_remap turns the hardware id into a logical id such that every XCD
+// runs one contiguous range of logical ids.
 __device__ __forceinline__ int xcd_remap(int h, int G) {
   const int per = G >> 3, rem = G & 7;
   const int x = h & 7, s = h >> 3;
   return x < rem ? x * (per + 1) + s : rem * (per + 1) + (x - rem) * per + s;
+}
+
+// Logical id -> (work item, panel).  Panels are taken in groups of
+// panel_group (about n_panels / 8, so that one XCD's range covers one group);
+// within a group the order is item-major.  An XCD then reads the B columns
+// of its group's panels only (they stay in its L2), and the panels of one
+// item run back to back on the same XCD, sharing the item's A tiles.
+__device__ __forceinline__ void wg_tile(int L, int n_items, int n_panels, int pgrp, int& item, int& panel) {
+  const int full = n_panels / pgrp;  // groups of exactly pgrp panels
+  const int gsize = n_items * pgrp;
+  int g = L / gsize;
+  int w = pgrp;
+  int r = L - g * gsize;
+  if (g >= full) {  // trailing group of n_panels % pgrp panels
+    g = full;
+    w = n_panels - full * pgrp;
+    r = L - full * gsize;
+  }
+  item = r / w;
+  panel = g * pgrp + (r - item * w);
 }
 
 // 4x4 byte transpose: r_i holds bytes (B[k+i][n+0..3]); c_n gets (B[k+0..3][n]).
@@ -93,36 +154,90 @@ __device__ __forceinline__ void transpose4x4(uint32_t r0, uint32_t r1, uint32_t 
   c3 = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
 }
 
-// Operand registers of one tile for one lane.
-struct Frag {
+// Raw operand registers of one tile for one lane, as loaded from memory.
+// Row-major B: r[i] holds B[k0+i][col0 .. col0+3] (one dword per row);
+// column-major B: r[4c+q] holds B[k0+4q .. k0+4q+3][col0+c].
+struct Raw {
   v4i a;
-  v4i b[kColsPerLane];  // b[c]: 16 k-contiguous bytes of column col0 + c
+  uint32_t r[16];
+  int krow;  // rows r[0 .. krow) lie inside K
 };
 
+// Issue the loads of tile t (block column kb) without consuming them.
+// Columns at or beyond N read a clamped valid address: they only feed MFMA
+// output columns that are never stored.  Rows at or beyond K read a clamped
+// valid row; they meet the zero padding of the A tile, and the fp8 path
+// zeroes them explicitly (a NaN code times zero is still NaN).
 template <bool BCOL, bool VEC>
-__device__ __forceinline__ void load_frag(const Params& p, int t, int j, int g, int col0, Frag& f) {
+__device__ __forceinline__ void load_raw(const Params& p, int t, int kb, int j, int g, int col0, Raw& f) {
   f.a = *reinterpret_cast<const v4i*>(p.tiles + (size_t)t * (kTile * kTile) + j * kTile + g * 16);
-  const int kb = p.col_idx[t];
   const int k0 = kb * kTile + g * 16;
-  const int krem = p.K - k0;  // rows of B that exist from k0 on
+  const bool kfull = kb * kTile + kTile <= p.K;  // uniform: the whole 32-row slab of B exists
+  f.krow = 16;
   if constexpr (!BCOL) {
-    const uint8_t* bp = p.b + (int64_t)k0 * p.ldb + col0;
-    uint32_t r[16];
     if constexpr (VEC) {
-      const bool colok = col0 < p.N;
+      const uint8_t* base = p.b + (col0 < p.N ? col0 : 0);
+      if (kfull) {
+        const uint8_t* bp = base + (int64_t)k0 * p.ldb;
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        r[i] = (colok && i < krem) ? *reinterpret_cast<const uint32_t*>(bp + i * p.ldb) : 0u;
+        for (int i = 0; i < 16; ++i) f.r[i] = *reinterpret_cast<const uint32_t*>(bp + i * p.ldb);
+      } else {
+        f.krow = p.K - k0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kk = k0 + i;
+          const int kc = kk < p.K ? kk : p.K - 1;
+          f.r[i] = *reinterpret_cast<const uint32_t*>(base + (int64_t)kc * p.ldb);
+        }
+      }
     } else {
+      const uint8_t* bp = p.b + (int64_t)k0 * p.ldb + col0;
+      const int krem = p.K - k0;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         uint32_t w = 0;
 #pragma unroll
         for (int c = 0; c < 4; ++c)
           if (i < krem && col0 + c < p.N) w |= (uint32_t)bp[i * p.ldb + c] << (8 * c);
-        r[i] = w;
+        f.r[i] = w;
       }
     }
+  } else {
+#pragma unroll
+    for (int c = 0; c < kColsPerLane; ++c) {
+      if constexpr (VEC) {
+        // Host guarantees K % 32 == 0, ldb % 16 == 0 and a 16-byte aligned b.
+        const int cc = col0 + c < p.N ? col0 + c : 0;
+        const v4i v = *reinterpret_cast<const v4i*>(p.b + (int64_t)cc * p.ldb + k0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) f.r[4 * c + q] = (uint32_t)v[q];
+      } else {
+        const uint8_t* bp = p.b + (int64_t)(col0 + c) * p.ldb + k0;
+        const int krem = p.K - k0;
+        uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (i < krem && col0 + c < p.N) w[i >> 2] |= (uint32_t)bp[i] << (8 * (i & 3));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) f.r[4 * c + q] = w[q];
+      }
+    }
+  }
+}
+
+// MFMA operands of one tile: b[c] = 16 k-contiguous bytes of column col0 + c.
+struct Frag {
+  v4i a;
+  v4i b[kColsPerLane];
+};
+
+template <int ELT, bool BCOL>
+__device__ __forceinline__ void to_frag(const Raw& raw, Frag& f) {
+  f.a = raw.a;
+  if constexpr (!BCOL) {
+    uint32_t r[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r[i] = (ELT == kEltFp8 && i >= raw.krow) ? 0u : raw.r[i];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       uint32_t c0, c1, c2, c3;
@@ -134,19 +249,9 @@ __device__ __forceinline__ void load_frag(const Params& p, int t, int j, int g, 
     }
   } else {
 #pragma unroll
-    for (int c = 0; c < kColsPerLane; ++c) {
-      const uint8_t* bp = p.b + (int64_t)(col0 + c) * p.ldb + k0;
-      if constexpr (VEC) {
-        // Host guarantees K % 32 == 0, ldb % 16 == 0 and a 16-byte aligned b.
-        f.b[c] = (col0 + c < p.N) ? *reinterpret_cast<const v4i*>(bp) : v4i{0, 0, 0, 0};
-      } else {
-        v4i w = {0, 0, 0, 0};
+    for (int c = 0; c < kColsPerLane; ++c)
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (i < krem && col0 + c < p.N) w[i >> 2] |= (int)((uint32_t)bp[i] << (8 * (i & 3)));
-        f.b[c] = w;
-      }
-    }
+      for (int q = 0; q < 4; ++q) f.b[c][q] = (int)raw.r[4 * c + q];
   }
 }
 
@@ -254,132 +359,348 @@ __device__ __forceinline__ void store4(const Params& p, int grow, int col, const
   }
 }
 
-template <int ELT, int EPI, int OUT, bool BCOL, bool VEC>
-__global__ __launch_bounds__(kThreads) void spmm_bsr_kernel(Params p) {
+// ---- B through LDS (row-major B, N and ldb multiples of 16) --------------
+// A tile's 32 x 128 B slab is read with four 16-byte loads per lane (lane l,
+// load q: row 8q + l/8, bytes 16*(l%8) .. +15 of the panel), written to the
+// wave's LDS slot, and read back k-contiguous with ds_read_b64_tr_b8: within
+// each 16-lane group, lane 2t supplies bytes 0..7 and lane 2t+1 bytes 8..15
+// of row t, and lane i receives column i of the 8 x 16 byte block.  The 16
+// byte chunks of a row are XOR-swizzled with the row index so that the eight
+// rows of one transposed read fall into different LDS banks.
+struct RawL {
+  v4i a;
+  v4i bq[4];
+};
+
+constexpr int kSlotBytes = kTile * kPanel;  // 4 KB: one B slab
+
+// live == false (a batch slot past the item's end): every lane reads the
+// same 16 bytes, so the slot costs one cache line but keeps the number of
+// outstanding loads fixed, which lets the compiler's vmcnt waits stay exact.
+template <int ELT>
+__device__ __forceinline__ void load_raw_lds(const Params& p, int t, int kb, bool live, int j, int g,
+                                             int lane, int panel_col, RawL& f) {
+  // Offsets are masked arithmetically (not selected) so that the compiler
+  // keeps these loads unconditional.
+  const int64_t m = -(int64_t)live;
+  f.a = *reinterpret_cast<const v4i*>(p.tiles + (((int64_t)t * (kTile * kTile) + j * kTile + g * 16) & m));
+  const int chunk_col = panel_col + 16 * (lane & 7);
+  const int col = chunk_col < p.N ? chunk_col : 0;  // past N: any valid chunk, never stored
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int k = kb * kTile + 8 * q + (lane >> 3);
+    const int kc = k < p.K ? k : p.K - 1;
+    f.bq[q] = *reinterpret_cast<const v4i*>(p.b + (((int64_t)kc * p.ldb + col) & m));
+  }
+}
+
+template <int ELT>
+__device__ __forceinline__ void stage_lds(const RawL& f, int kb, int K, int lane, uint8_t* slot) {
+  const int kmax = K - kb * kTile;  // rows of the slab inside K
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int rowl = 8 * q + (lane >> 3);
+    v4i v = f.bq[q];
+    if (ELT == kEltFp8 && rowl >= kmax) v = v4i{0, 0, 0, 0};  // rows past K: fp8 codes may be NaN
+    *reinterpret_cast<v4i*>(slot + rowl * kPanel + ((((lane & 7) ^ (rowl & 7))) << 4)) = v;
+  }
+}
+
+__device__ __forceinline__ v4i read_tr(const uint8_t* slot, int c, int j, int g) {
+  const int i = j & 15;
+  const int s = 2 * c + (j >> 4);
+  v4i out;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int rowl = 16 * g + 8 * h + (i >> 1);
+    const uint8_t* a = slot + rowl * kPanel + ((s ^ (rowl & 7)) << 4) + 8 * (i & 1);
+    typedef int v2i __attribute__((ext_vector_type(2)));
+    const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+        (__attribute__((address_space(3))) v2i*)(const_cast<uint8_t*>(a)));
+    out[2 * h] = v[0];
+    out[2 * h + 1] = v[1];
+  }
+  return out;
+}
+
+__device__ __forceinline__ float bcast(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Row stride (dwords) of the LDS reduction buffer: 128 columns + 4 of padding
+// keep the two row halves a wave writes in one instruction in different banks.
+constexpr int kRedStride = kPanel + 32;  // also makes each wave's region hold kBatch B slabs
+
+// Column position of (row, col) in the reduction buffer: rows 4 apart (the
+// two halves of one MFMA result write) sit 16 banks apart.
+__device__ __forceinline__ int red_col(int row, int col) { return col ^ (((row >> 2) & 1) << 4); }
+
+template <int ELT, int EPI, int OUT, bool BCOL, bool VEC, bool LDSB>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void spmm_bsr_kernel(Params p) {
   using A = Accum<ELT, EPI>;
   using Reg = typename A::Reg;
   constexpr bool kInt = A::kInt;
 
-  __shared__ v4i red[kWaves][kTile][kPanel / 4];  // 64 KB: per-wave 32 x 128 partials
-  __shared__ int s_last;
+  // Per wave: 32 x 132 dwords of partial sums; during the tile loop the same
+  // bytes hold the wave's kBatch B slabs (LDSB path).
+  __shared__ __attribute__((aligned(16))) int red[kWaves][kTile][kRedStride];
+  int& s_last = red[0][0][kPanel];  // padding word: split-row arrival flag
+  static_assert(kBatch * kSlotBytes <= (int)sizeof(red[0]), "B slabs must fit the wave's LDS region");
 
+  TRACE_DECL;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int j = lane & 31, g = lane >> 5;
 
   const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-  const int item_idx = L / p.n_panels;
-  const int panel = L - item_idx * p.n_panels;
-  const void_work_item it = p.items[item_idx];
+  int item_idx, panel;
+  wg_tile(L, p.n_items, p.n_panels, p.panel_group, item_idx, panel);
+  const void_work_item* itp = p.items + item_idx;
+  // Block columns of the first batch (tiles wave + 4u, u < 4) through the
+  // scalar cache, issued together with the record's fields: a cold scalar
+  // load returns well before a cold vector load.
+  const v4i* colv = reinterpret_cast<const v4i*>(itp->cols);
+  const v4i cq0 = colv[0], cq1 = colv[1], cq2 = colv[2], cq3 = colv[3], cq4 = colv[4];
+  __builtin_amdgcn_sched_barrier(0);
+  const int row = itp->row, begin = itp->begin, end = itp->end, split_tile = itp->tile;
   const int col0 = panel * kPanel + j * kColsPerLane;
+  (void)(row + begin + end);
+  TRACE_POINT(0);
+
+  // Load order matters: vmcnt retires vector loads in issue order, so a
+  // value is usable only once every load issued before it has returned.
+  // (1) the first batch's block columns (from the item record, lanes <
+  //     kInline) and per-tile scales, (2) the first batch's A and B tiles,
+  // (3) what is needed later: columns of further tiles, B scales, bias and
+  //     the row-mean scales.
+  // Tiles of the item are taken round-robin by the waves (wave w: tiles w,
+  // w+4, ...); columns past the item's end are -1 and are clamped to a
+  // valid address, their products skipped.
+  const int nt = end - begin;
+  const int tl = begin + min(lane, max(nt - 1, 0));
+  float my_scale = 0.f;
+  if constexpr (EPI == VOID_EPI_PER_BLOCK) my_scale = p.per_tensor_a ? p.a_scale[0] : p.a_scale[tl];
+  auto scale_of = [&](int idx) -> float {
+    if constexpr (EPI != VOID_EPI_PER_BLOCK) return 0.f;
+    if (idx < 64) return bcast(my_scale, idx);
+    return p.per_tensor_a ? p.a_scale[0] : p.a_scale[begin + idx];
+  };
 
   Reg acc[kColsPerLane];
 #pragma unroll
   for (int c = 0; c < kColsPerLane; ++c) acc[c] = Reg{};
 
-  // Software pipeline: the next tile's loads are in flight while the current
-  // tile's MFMAs run.
-  int t = it.begin + wave;
-  Frag cur, nxt;
-  if (t < it.end) load_frag<BCOL, VEC>(p, t, j, g, col0, cur);
-  while (t < it.end) {
-    const int tn = t + kWaves;
-    if (tn < it.end) load_frag<BCOL, VEC>(p, tn, j, g, col0, nxt);
-    const float s = (EPI == VOID_EPI_PER_BLOCK) ? (p.per_tensor_a ? p.a_scale[0] : p.a_scale[t]) : 0.f;
-    A::step(acc, cur, s);
-    cur = nxt;
-    t = tn;
+  const int col_64 = nt > 0 ? p.col_idx[tl] : 0;  // before the tile loads: vmcnt retires in order
+  const bool has_first = wave < nt;
+  const v4i cq[5] = {cq0, cq1, cq2, cq3, cq4};
+  static_assert(kBatch <= 5 && kBatch * kWaves <= kInline, "first batch columns come from the record");
+  int kbs0[kBatch];
+#pragma unroll
+  for (int u = 0; u < kBatch; ++u)
+    kbs0[u] = max(wave == 0 ? cq[u][0] : wave == 1 ? cq[u][1] : wave == 2 ? cq[u][2] : cq[u][3], 0);
+
+  // Operand loading differs by B layout; everything else is shared.
+  using RawT = typename std::conditional<LDSB, RawL, Raw>::type;
+  uint8_t* stage = reinterpret_cast<uint8_t*>(&red[wave][0][0]);
+  auto issue = [&](RawT& r, int idx, int kb) {
+    const bool live = idx < nt;
+    const int t = begin + (live ? idx : 0);
+    if constexpr (LDSB) load_raw_lds<ELT>(p, t, live ? kb : 0, live, j, g, lane, panel * kPanel, r);
+    else load_raw<BCOL, VEC>(p, t, live ? kb : 0, j, g, col0, r);
+  };
+  auto consume = [&](const RawT& r, int kb, int u, int idx, float sc) {
+    Frag f;
+    if constexpr (LDSB) {
+      uint8_t* slot = stage + u * kSlotBytes;
+      stage_lds<ELT>(r, kb, p.K, lane, slot);
+      f.a = r.a;
+#pragma unroll
+      for (int c = 0; c < kColsPerLane; ++c) f.b[c] = read_tr(slot, c, j, g);
+    } else {
+      to_frag<ELT, BCOL>(r, f);
+    }
+    A::step(acc, f, sc);
+  };
+
+  RawT raw0[kBatch];
+  if (has_first) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) issue(raw0[u], wave + u * kWaves, kbs0[u]);
   }
+  TRACE_POINT(1);
+
+  // Epilogue inputs, issued after the first tiles' loads.
+  // Branch-free (a load under a branch would make the vmcnt waits above
+  // conservative): absent vectors read a_scale[0] and are then ignored.
+  float sb[4], bias[4];
+  {
+    const float* sbp = p.b_scale_vec ? p.b_scale_vec : p.a_scale;
+    const float* bip = p.bias ? p.bias : p.a_scale;
+    const int cmax = (p.b_scale_vec || p.bias) ? p.N - 1 : 0;
+    float vs[4], vb[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int cc = min(col0 + c, cmax);
+      vs[c] = sbp[p.b_scale_vec ? cc : 0];
+      vb[c] = bip[p.bias ? cc : 0];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      sb[c] = p.b_scale_vec ? vs[c] : p.b_scale;
+      bias[c] = p.bias ? vb[c] : 0.f;
+    }
+  }
+  int rb = 0, re = 0;
+  float row_scale = 0.f;  // a_scale of the row's first 64 tiles, one per lane (row-mean)
+  if constexpr (EPI == VOID_EPI_ROW_MEAN) {
+    // An unsplit item is its whole block-row; a split row needs row_ptr.
+    if (split_tile < 0) {
+      rb = begin;
+      re = end;
+      row_scale = p.per_tensor_a ? p.a_scale[0] : p.a_scale[tl];
+    } else {
+      rb = p.row_ptr[row];
+      re = p.row_ptr[row + 1];
+      row_scale = p.per_tensor_a ? p.a_scale[0] : p.a_scale[rb + min(lane, max(re - rb - 1, 0))];
+    }
+  }
+
+  if (has_first) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int idx = wave + u * kWaves;
+      // idx < kBatch * kWaves < 64: the scale comes from my_scale without the
+      // branch of scale_of (a branch here would blur the compiler's vmcnt count).
+      if (idx < nt) consume(raw0[u], kbs0[u], u, idx, EPI == VOID_EPI_PER_BLOCK ? bcast(my_scale, idx) : 0.f);
+    }
+  }
+  // Further rounds (items longer than kBatch * kWaves tiles).
+  for (int base = wave + kBatch * kWaves; base < nt; base += kBatch * kWaves) {
+    int kbs[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int idx = base + u * kWaves;
+      const int ii = idx < nt ? idx : base;  // empty slots reload a valid tile and are skipped
+      kbs[u] = ii < 64 ? __builtin_amdgcn_readlane(col_64, ii) : p.col_idx[begin + ii];
+    }
+    RawT raw[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) issue(raw[u], base + u * kWaves, kbs[u]);
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int idx = base + u * kWaves;
+      if (idx < nt) consume(raw[u], kbs[u], u, idx, scale_of(idx));
+    }
+  }
+
+  TRACE_POINT(2);
 
   // Cross-wave reduction.  MFMA 32x32 result layout: lane l, register r holds
   // row 8*(r/4) + 4*(l/32) + r%4 of virtual column l%32.
+  // LDSB: MFMA c holds columns 32c + j; otherwise columns 4j + c.
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const int row = 8 * (r >> 2) + 4 * g + (r & 3);
-    v4i w;
+    const int rr = 8 * (r >> 2) + 4 * g + (r & 3);
+    if constexpr (LDSB) {
 #pragma unroll
-    for (int c = 0; c < kColsPerLane; ++c) w[c] = kInt ? (int)acc[c][r] : __float_as_int((float)acc[c][r]);
-    red[wave][row][j] = w;
+      for (int c = 0; c < kColsPerLane; ++c)
+        red[wave][rr][red_col(rr, 32 * c + j)] = kInt ? (int)acc[c][r] : __float_as_int((float)acc[c][r]);
+    } else {
+      v4i w;
+#pragma unroll
+      for (int c = 0; c < kColsPerLane; ++c) w[c] = kInt ? (int)acc[c][r] : __float_as_int((float)acc[c][r]);
+      *reinterpret_cast<v4i*>(&red[wave][rr][red_col(rr, 4 * j)]) = w;
+    }
   }
   __syncthreads();
 
   // Epilogue ownership: wave w finishes rows [8w, 8w+8); lane owns columns
   // col0 .. col0+3 (same j as above) of rows 8w + g + 2i.
-  constexpr int kRowsPerWave = kTile / kWaves;
   v4i sumi[kRowsPerWave / 2];
   v4f sumf[kRowsPerWave / 2];
 #pragma unroll
   for (int i = 0; i < kRowsPerWave / 2; ++i) {
-    const int row = wave * kRowsPerWave + 2 * i + g;
+    const int rr = wave * kRowsPerWave + 2 * i + g;
     v4i si = {0, 0, 0, 0};
     v4f sf = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const v4i x = red[w][row][j];
+      const v4i x = *reinterpret_cast<const v4i*>(&red[w][rr][red_col(rr, 4 * j)]);
       if constexpr (kInt) si += x;
       else sf += v4f{__int_as_float(x[0]), __int_as_float(x[1]), __int_as_float(x[2]), __int_as_float(x[3])};
     }
     sumi[i] = si;
     sumf[i] = sf;
   }
+  TRACE_POINT(3);
 
-  if (it.tile >= 0) {
-    // Split row: publish this chunk's partial tile, count arrivals, and let
-    // the last chunk reduce all partials in chunk order.
+  if (itp->tile >= 0) {
+    // Split row: publish this chunk's partial tile with agent-coherent (sc1)
+    // stores, count arrivals, and let the last chunk read every partial back
+    // with agent-coherent loads and reduce them in chunk order.  Coherent
+    // accesses replace release/acquire fences, which would write back and
+    // invalidate the whole L2 of the XCD.
+    const int tile_id = itp->tile, nchunks = itp->nchunks, slot = itp->slot, chunk = itp->chunk;
     const size_t tile_elems = (size_t)kTile * kPanel;
-    v4i* part = static_cast<v4i*>(p.partials);
+    int* part = static_cast<int*>(p.partials);
 #pragma unroll
     for (int i = 0; i < kRowsPerWave / 2; ++i) {
-      const int row = wave * kRowsPerWave + 2 * i + g;
-      const size_t off = ((size_t)(it.slot + it.chunk) * p.n_panels + panel) * tile_elems + (size_t)row * kPanel;
-      v4i w;
-      if constexpr (kInt) w = sumi[i];
-      else w = v4i{__float_as_int(sumf[i][0]), __float_as_int(sumf[i][1]), __float_as_int(sumf[i][2]), __float_as_int(sumf[i][3])};
-      part[(off >> 2) + j] = w;
+      const int rr = wave * kRowsPerWave + 2 * i + g;
+      const size_t off = ((size_t)(slot + chunk) * p.n_panels + panel) * tile_elems + (size_t)rr * kPanel + 4 * j;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int w = kInt ? sumi[i][c] : __float_as_int(sumf[i][c]);
+        __hip_atomic_store(part + off + c, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are acknowledged
     __syncthreads();
-    unsigned* ctr = p.counters + (size_t)it.tile * p.n_panels + panel;
+    unsigned* ctr = p.counters + (size_t)tile_id * p.n_panels + panel;
     if (tid == 0) {
-      const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = (old == (unsigned)(it.nchunks - 1));
+      const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = (old == (unsigned)(nchunks - 1));
     }
     __syncthreads();
-    if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (!s_last) {
+      TRACE_FLUSH();
+      return;
+    }
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
     for (int i = 0; i < kRowsPerWave / 2; ++i) {
-      const int row = wave * kRowsPerWave + 2 * i + g;
+      const int rr = wave * kRowsPerWave + 2 * i + g;
       v4i si = {0, 0, 0, 0};
       v4f sf = {0.f, 0.f, 0.f, 0.f};
-      for (int ch = 0; ch < it.nchunks; ++ch) {
-        const size_t off = ((size_t)(it.slot + ch) * p.n_panels + panel) * tile_elems + (size_t)row * kPanel;
-        const v4i x = __builtin_nontemporal_load(&part[(off >> 2) + j]);
-        if constexpr (kInt) si += x;
-        else sf += v4f{__int_as_float(x[0]), __int_as_float(x[1]), __int_as_float(x[2]), __int_as_float(x[3])};
+      for (int ch = 0; ch < nchunks; ++ch) {
+        const size_t off = ((size_t)(slot + ch) * p.n_panels + panel) * tile_elems + (size_t)rr * kPanel + 4 * j;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int x = __hip_atomic_load(part + off + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if constexpr (kInt) si[c] += x;
+          else sf[c] += __int_as_float(x);
+        }
       }
       sumi[i] = si;
       sumf[i] = sf;
     }
   }
 
-  // Per-column B scale of this lane's four columns.
-  float sb[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-    sb[c] = p.b_scale_vec ? (col0 + c < p.N ? p.b_scale_vec[col0 + c] : 0.f) : p.b_scale;
-
   float mul[4] = {1.f, 1.f, 1.f, 1.f};
   if constexpr (EPI == VOID_EPI_ROW_MEAN) {
-    // int_quant.py:519-526: S = sum fl(s_a * s_b) in tile order, then S / n.
-    const int rb = p.row_ptr[it.row], re = p.row_ptr[it.row + 1];
+    // int_quant.py:519-526: S = sum fl(s_a * s_b) in tile order over the
+    // whole block-row, then S / n.  The row's scales sit one per lane and
+    // are folded sequentially with readlane.
     float S[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int tt = rb; tt < re; ++tt) {
-      const float sa = p.per_tensor_a ? p.a_scale[0] : p.a_scale[tt];
+    for (int t0 = rb; t0 < re; t0 += 64) {
+      const int n = min(64, re - t0);
+      const float mine = t0 == rb ? row_scale
+                                  : (p.per_tensor_a ? p.a_scale[0] : p.a_scale[t0 + min(lane, n - 1)]);
+      for (int q = 0; q < n; ++q) {
+        const float sa = bcast(mine, q);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) S[c] = __fadd_rn(S[c], __fmul_rn(sa, sb[c]));
+        for (int c = 0; c < 4; ++c) S[c] = __fadd_rn(S[c], __fmul_rn(sa, sb[c]));
+      }
     }
     const float n = (float)(re - rb);
 #pragma unroll
@@ -388,16 +709,11 @@ __global__ __launch_bounds__(kThreads) void spmm_bsr_kernel(Params p) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) mul[c] = sb[c];
   }
-  float bias[4] = {0.f, 0.f, 0.f, 0.f};
-  if (p.bias) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) bias[c] = (col0 + c < p.N) ? p.bias[col0 + c] : 0.f;
-  }
 
 #pragma unroll
   for (int i = 0; i < kRowsPerWave / 2; ++i) {
-    const int row = wave * kRowsPerWave + 2 * i + g;
-    const int grow = it.row * kTile + row;
+    const int rr = wave * kRowsPerWave + 2 * i + g;
+    const int grow = row * kTile + rr;
     float v[4];
     int vi[4];
 #pragma unroll
@@ -412,6 +728,8 @@ __global__ __launch_bounds__(kThreads) void spmm_bsr_kernel(Params p) {
     }
     store4<OUT, VEC>(p, grow, col0, v, vi);
   }
+  TRACE_POINT(4);
+  TRACE_FLUSH();
 }
 
 // ---------------------------------------------------------------------------
@@ -427,26 +745,36 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-template <int ELT, int EPI, int OUT, bool BCOL, bool VEC>
+template <int ELT, int EPI, int OUT, bool BCOL, bool VEC, bool LDSB = false>
 int launch(const Params& p, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((spmm_bsr_kernel<ELT, EPI, OUT, BCOL, VEC>), dim3(grid), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((spmm_bsr_kernel<ELT, EPI, OUT, BCOL, VEC, LDSB>), dim3(grid), dim3(kThreads), 0, stream, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(VOID_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
   return VOID_OK;
 }
 
+// B layouts: column-major (direct 16-byte loads), row-major through LDS
+// (16-byte aligned rows), row-major with in-register transposes (4-byte
+// aligned rows), or bytewise (anything else).
+enum Layout { kColVec, kColByte, kRowLds, kRowVec, kRowByte };
+
 template <int ELT, int EPI, int OUT>
-int launch_layout(const Params& p, int grid, hipStream_t s, bool bcol, bool vec) {
-  if (bcol) return vec ? launch<ELT, EPI, OUT, true, true>(p, grid, s) : launch<ELT, EPI, OUT, true, false>(p, grid, s);
-  return vec ? launch<ELT, EPI, OUT, false, true>(p, grid, s) : launch<ELT, EPI, OUT, false, false>(p, grid, s);
+int launch_layout(const Params& p, int grid, hipStream_t s, int layout) {
+  switch (layout) {
+    case kColVec: return launch<ELT, EPI, OUT, true, true>(p, grid, s);
+    case kColByte: return launch<ELT, EPI, OUT, true, false>(p, grid, s);
+    case kRowLds: return launch<ELT, EPI, OUT, false, true, true>(p, grid, s);
+    case kRowVec: return launch<ELT, EPI, OUT, false, true>(p, grid, s);
+    default: return launch<ELT, EPI, OUT, false, false>(p, grid, s);
+  }
 }
 
 template <int ELT, int EPI>
-int launch_out(const Params& p, int grid, hipStream_t s, bool bcol, bool vec, int out) {
+int launch_out(const Params& p, int grid, hipStream_t s, int layout, int out) {
   switch (out) {
-    case VOID_DT_F32: return launch_layout<ELT, EPI, VOID_DT_F32>(p, grid, s, bcol, vec);
-    case VOID_DT_BF16: return launch_layout<ELT, EPI, VOID_DT_BF16>(p, grid, s, bcol, vec);
-    case VOID_DT_F16: return launch_layout<ELT, EPI, VOID_DT_F16>(p, grid, s, bcol, vec);
+    case VOID_DT_F32: return launch_layout<ELT, EPI, VOID_DT_F32>(p, grid, s, layout);
+    case VOID_DT_BF16: return launch_layout<ELT, EPI, VOID_DT_BF16>(p, grid, s, layout);
+    case VOID_DT_F16: return launch_layout<ELT, EPI, VOID_DT_F16>(p, grid, s, layout);
     default: return fail(VOID_ERR_UNSUPPORTED, "out_dtype %d not supported with this epilogue", out);
   }
 }
@@ -456,6 +784,8 @@ size_t counters_bytes(int32_t n_split_tiles, int32_t n_panels) {
 }
 
 int n_panels_for(int32_t N) { return (N + kPanel - 1) / kPanel; }
+
+unsigned long long* g_trace = nullptr;  // set by void_debug_set_trace in instrumented builds
 
 int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilogue,
         const void_plan* plan, void* workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -507,7 +837,10 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
   p.K = a->K;
   p.n_panels = n_panels;
   p.activation = d->activation;
+  p.n_items = n_items;
+  p.panel_group = n_panels >= 16 ? n_panels / 8 : 1;
   p.items = items;
+  p.trace = g_trace;
   if (n_split_tiles > 0) {
     if (!workspace) return fail(VOID_ERR_WORKSPACE, "plan splits rows but workspace is null");
     const size_t need = void_workspace_bytes(n_split_tiles, plan->n_slots, d->N);
@@ -519,28 +852,32 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
 
   const uintptr_t bu = (uintptr_t)d->b, cu = (uintptr_t)d->c;
   const bool c_ok = (cu % 16 == 0) && (d->ldc % 4 == 0) && (d->N % 4 == 0);
-  bool vec;
+  int layout;
   if (d->b_col_major)
-    vec = c_ok && (bu % 16 == 0) && (d->ldb % 16 == 0) && (a->K % kTile == 0);
+    layout = (c_ok && (bu % 16 == 0) && (d->ldb % 16 == 0) && (a->K % kTile == 0)) ? kColVec : kColByte;
+  else if (c_ok && (bu % 16 == 0) && (d->ldb % 16 == 0) && (d->N % 16 == 0))
+    layout = kRowLds;
   else
-    vec = c_ok && (bu % 4 == 0) && (d->ldb % 4 == 0);
-  const bool bcol = d->b_col_major != 0;
+    layout = (c_ok && (bu % 4 == 0) && (d->ldb % 4 == 0)) ? kRowVec : kRowByte;
   const int grid = (int)grid64;
 
   if (elt == kEltI8) {
     switch (epilogue) {
       case VOID_EPI_RAW_I32:
-        return bcol ? (vec ? launch<kEltI8, VOID_EPI_RAW_I32, VOID_DT_I32, true, true>(p, grid, stream)
-                           : launch<kEltI8, VOID_EPI_RAW_I32, VOID_DT_I32, true, false>(p, grid, stream))
-                    : (vec ? launch<kEltI8, VOID_EPI_RAW_I32, VOID_DT_I32, false, true>(p, grid, stream)
-                           : launch<kEltI8, VOID_EPI_RAW_I32, VOID_DT_I32, false, false>(p, grid, stream));
+        switch (layout) {
+          case kColVec: return launch<kEltI8, VOID_EPI_RAW_I32, VOID_DT_I32, true, true>(p, grid, stream);
+          case kColByte: return launch<kEltI8, VOID_EPI_RAW_I32, VOID_DT_I32, true, false>(p, grid, stream);
+          case kRowLds: return launch<kEltI8, VOID_EPI_RAW_I32, VOID_DT_I32, false, true, true>(p, grid, stream);
+          case kRowVec: return launch<kEltI8, VOID_EPI_RAW_I32, VOID_DT_I32, false, true>(p, grid, stream);
+          default: return launch<kEltI8, VOID_EPI_RAW_I32, VOID_DT_I32, false, false>(p, grid, stream);
+        }
       case VOID_EPI_ROW_MEAN:
-        return launch_out<kEltI8, VOID_EPI_ROW_MEAN>(p, grid, stream, bcol, vec, d->out_dtype);
+        return launch_out<kEltI8, VOID_EPI_ROW_MEAN>(p, grid, stream, layout, d->out_dtype);
       default:
-        return launch_out<kEltI8, VOID_EPI_PER_BLOCK>(p, grid, stream, bcol, vec, d->out_dtype);
+        return launch_out<kEltI8, VOID_EPI_PER_BLOCK>(p, grid, stream, layout, d->out_dtype);
     }
   }
-  return launch_out<kEltFp8, VOID_EPI_PER_BLOCK>(p, grid, stream, bcol, vec, d->out_dtype);
+  return launch_out<kEltFp8, VOID_EPI_PER_BLOCK>(p, grid, stream, layout, d->out_dtype);
 }
 
 }  // namespace
@@ -553,28 +890,47 @@ const char* void_last_error(void) { return g_err; }
 
 int void_panel_width(void) { return kPanel; }
 
-int void_streamk_plan(const int32_t* row_ptr, int32_t n_block_rows, int32_t chunk_tiles,
-                      void_work_item* items, int32_t capacity, int32_t* n_items,
-                      int32_t* n_split_tiles, int32_t* n_slots) {
+#ifdef VOID_TRACE
+// Instrumented builds only: every launch records 8 realtime stamps per
+// workgroup into buf (device memory, >= 8 * grid entries).
+void void_debug_set_trace(unsigned long long* buf) { g_trace = buf; }
+#endif
+
+int void_streamk_plan(const int32_t* row_ptr, const int32_t* col_idx, int32_t n_block_rows,
+                      int32_t chunk_tiles, void_work_item* items, int32_t capacity,
+                      int32_t* n_items, int32_t* n_split_tiles, int32_t* n_slots) {
   g_err[0] = 0;
   if (!row_ptr || !n_items || !n_split_tiles || !n_slots || n_block_rows < 0 || chunk_tiles < 1)
     return fail(VOID_ERR_ARG, "bad planner arguments");
   std::vector<void_work_item> out;
   out.reserve(n_block_rows);
   int32_t tiles = 0, slots = 0;
+  auto make = [&](int32_t r, int32_t b, int32_t e, int32_t tile, int32_t nch, int32_t ch, int32_t slot) {
+    void_work_item w;
+    w.row = r;
+    w.begin = b;
+    w.end = e;
+    w.tile = tile;
+    w.nchunks = nch;
+    w.chunk = ch;
+    w.slot = slot;
+    w.reserved = 0;
+    for (int i = 0; i < VOID_ITEM_INLINE_COLS; ++i) w.cols[i] = (col_idx && b + i < e) ? col_idx[b + i] : -1;
+    out.push_back(w);
+  };
   for (int32_t r = 0; r < n_block_rows; ++r) {
     const int32_t b = row_ptr[r], e = row_ptr[r + 1];
     if (e < b) return fail(VOID_ERR_ARG, "row_ptr decreases at row %d", r);
     const int32_t n = e - b;
     if (n <= chunk_tiles) {
-      out.push_back(void_work_item{r, b, e, -1, 1, 0, 0, 0});
+      make(r, b, e, -1, 1, 0, 0);
       continue;
     }
     const int32_t nch = (n + chunk_tiles - 1) / chunk_tiles;
     for (int32_t c = 0; c < nch; ++c) {
       const int32_t cb = b + (int32_t)((int64_t)c * n / nch);
       const int32_t ce = b + (int32_t)((int64_t)(c + 1) * n / nch);
-      out.push_back(void_work_item{r, cb, ce, tiles, nch, c, slots, 0});
+      make(r, cb, ce, tiles, nch, c, slots);
     }
     tiles += 1;
     slots += nch;

@@ -5,13 +5,17 @@ a JSON cache (void/autotune.py:39-104, 345-381).  On MI355X the kernel shape
 is fixed by the hardware instead:
 
 * one workgroup = 4 wave64s, one 32-row block-row x 128-column panel of C,
-  64 KB of LDS for the cross-wave reduction -> 2 workgroups per CU;
+  80 KB of LDS (B slabs during the tile loop, then the cross-wave
+  reduction) -> 2 workgroups per CU;
 * 256 CUs in 8 XCDs -> 512 resident workgroups;
 * the only shape-dependent knob is the Stream-K chunk: the most tiles one
-  work item may take before its block-row is split.  It is the larger of a
-  floor (splitting costs a partial-tile round trip through L2) and the
-  average work per resident workgroup, so that no item is longer than the
-  average load of a workgroup slot.
+  work item may take before its block-row is split.  A split row pays for
+  a partial-tile round trip through memory (coherent stores, an atomic,
+  coherent loads: several microseconds), while an unsplit workgroup takes
+  20 tiles per round of loads (4 waves x 5 tiles).  The chunk is therefore
+  the larger of a floor of 64 tiles (about three rounds) and the average
+  work per resident workgroup slot: only rows far longer than the typical
+  item are split.
 """
 
 from __future__ import annotations
@@ -27,8 +31,8 @@ TILE = 32
 
 # (name, floor on the chunk, factor on the per-slot average)
 CHUNK_TABLE = {
-    "int8": (16, 1.0),
-    "fp8": (16, 1.0),
+    "int8": (64, 1.0),
+    "fp8": (64, 1.0),
 }
 
 
