@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--chunk", type=int, default=None, help="override the Stream-K chunk")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--profile", action="store_true", help="no CPU leg, no flush: for rocprofv3 runs")
+    ap.add_argument("--counters", action="store_true",
+                    help="eager launches for rocprofv3 --pmc: each step overwrites 1 GiB, copies a "
+                         "64 MiB calibration buffer, then runs the SpMM; prints no JSON line")
     return ap.parse_args()
 
 
@@ -177,6 +180,22 @@ def time_gpu(prob, steps: int, warmup: int, flush: bool):
     return cold, hot, wall
 
 
+def run_for_counters(prob, steps: int):
+    """Eager sequence for HBM-traffic counters (no graph: per-dispatch counters
+    need one dispatch per kernel).  Per step: a 1 GiB overwrite (cold L2 and
+    Infinity Cache), a plain 64 MiB device-to-device copy whose FETCH_SIZE and
+    WRITE_SIZE calibrate the counters against a known byte count, and the SpMM."""
+    import torch
+    scratch = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+    src = torch.ones(1 << 24, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for i in range(steps):
+        scratch.fill_(float(i))
+        dst.copy_(src)
+        prob["run"]()
+    torch.cuda.synchronize()
+
+
 def time_cpu(prob, budget_s: float):
     import torch
 
@@ -207,6 +226,9 @@ def main():
     prob = build_problem(args.config, dev, args.epilogue)
     if args.chunk:
         prob["chunk"] = args.chunk
+    if args.counters:
+        run_for_counters(prob, args.steps)
+        return
     cold, hot, wall = time_gpu(prob, args.steps, args.warmup, flush=not args.profile)
     t_ms = cold if cold is not None else hot
     tops = prob["ops"] / (t_ms * 1e-3) / 1e12

@@ -200,5 +200,5 @@ def test_analyze_workload_balance():
 
 def test_chunk_table():
     assert tuning.select_chunk("int8", 1638, 512) == 64                       # c2: no split
-    assert tuning.select_chunk("int8", 17960, 256) == 71                      # c4: per-slot average
+    assert tuning.select_chunk("int8", 17960, 256) == 64                      # c4: capped at 64
     assert tuning.n_panels(512) == 4 and tuning.n_panels(130) == 2

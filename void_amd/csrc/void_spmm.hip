@@ -34,6 +34,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <type_traits>
 #include <vector>
@@ -753,6 +754,373 @@ int launch(const Params& p, int grid, hipStream_t stream) {
   return VOID_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Column-group kernel: row-major B with 16-byte aligned rows, or
+// column-major B with K % 32 == 0.
+//
+// One workgroup = 4 wave64s = one work item x one 128-column panel, as for
+// spmm_bsr_kernel, but every wave runs all of the item's tiles for its own 32
+// output columns (column group cg = 4 * panel + wave), so no cross-wave
+// reduction is needed.  Tiles go in batches of kCgBatch, staged through a
+// double-buffered LDS area with one barrier per batch:
+//  - A: each wave loads two of the batch's tiles (MFMA fragment order);
+//  - row-major B: each wave loads 8 of the 32 rows of every tile's
+//    32 x 128 slab (full 128-byte lines), written with the same XOR chunk
+//    swizzle as stage_lds; every wave then reads its own 32 columns back
+//    k-contiguous with ds_read_b64_tr_b8 (read_tr);
+//  - column-major B: each wave loads its MFMA operands directly.
+// The loads of batch b + 1 are in flight while batch b is multiplied, and
+// every tile-dependent address is a wave-uniform buffer offset (SGPR), so
+// the tile loop spends no vector ALU work on addressing.
+// A work item has at most kCgMaxTiles tiles: the block columns of batches 0
+// and 1 come with the work item, the rest and the per-tile scales are one
+// dword per lane of a single load issued before the first batch.
+constexpr int kCgBatch = 8;
+constexpr int kCgAPerWave = kCgBatch / kWaves;
+constexpr int kCgMaxTiles = 64;
+static_assert(2 * kCgBatch <= kInline, "the first two batches' columns come from the work item");
+
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+
+__device__ __forceinline__ Rsrc make_rsrc(const void* p) {
+  // Raw buffer (stride 0) over the whole 32-bit offset range; the host
+  // checks that every operand's offsets fit in 31 bits.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, -1, 0x00020000);
+}
+
+// One tile's MFMA operands for a single 32-column group.
+struct Frag1 {
+  v4i a;
+  v4i b;
+};
+
+template <int ELT, int EPI>
+struct Accum1;
+
+template <int EPI>
+struct Accum1<kEltI8, EPI> {
+  static constexpr bool kInt = (EPI != VOID_EPI_PER_BLOCK);
+  using Reg = typename std::conditional<kInt, v16i, v16f>::type;
+  __device__ __forceinline__ static void step(Reg& acc, const Frag1& f, float s) {
+    if constexpr (kInt) {
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a, f.b, acc, 0, 0, 0);
+    } else {
+      const v16i z = {};
+      const v16i part = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a, f.b, z, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = __builtin_fmaf(s, (float)part[r], acc[r]);
+    }
+  }
+};
+
+template <int EPI>
+struct Accum1<kEltFp8, EPI> {
+  static constexpr bool kInt = false;
+  using Reg = v16f;
+  __device__ __forceinline__ static void step(Reg& acc, const Frag1& f, float s) {
+    const v16f z = {};
+    v16f part = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(pack2(f.a[0], f.a[1]), pack2(f.b[0], f.b[1]), z, 0, 0, 0);
+    part = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(pack2(f.a[2], f.a[3]), pack2(f.b[2], f.b[3]), part, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = __builtin_fmaf(s, part[r], acc[r]);
+  }
+};
+
+struct CgBatch {
+  v4i a[kCgAPerWave];  // A tiles wave + 4q of the batch, lane (j, g): row j, bytes 16g .. 16g+15
+  v4i b[kCgBatch];     // row-major B: slab row 8 wave + lane / 8, bytes 16 (lane % 8) .. +15;
+                       // column-major B: the MFMA operand (column j, rows 16g .. 16g+15)
+  int last_mask;       // bit u: tile u's slab is the one that crosses K
+};
+
+template <int ELT, int EPI, int OUT, bool BCOL>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void spmm_cg_kernel(Params p) {
+  using A = Accum1<ELT, EPI>;
+  constexpr bool kInt = A::kInt;
+  constexpr bool kScales = (EPI == VOID_EPI_PER_BLOCK);
+
+  __shared__ __attribute__((aligned(16))) v4i a_lds[2][kCgBatch][64];
+  __shared__ __attribute__((aligned(16))) uint8_t b_lds[BCOL ? 1 : 2][BCOL ? 1 : kCgBatch][BCOL ? 16 : kSlotBytes];
+  // Split-row arrival flag: the first word of the A area, free once every
+  // wave has passed the tile loop (80 KB in total keeps two workgroups per CU).
+  int& s_last = *reinterpret_cast<int*>(&a_lds[0][0][0]);
+
+  TRACE_DECL;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int j = lane & 31, g = lane >> 5;
+
+  const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  int item_idx, panel;
+  wg_tile(L, p.n_items, p.n_panels, p.panel_group, item_idx, panel);
+  const void_work_item* itp = p.items + item_idx;
+  const v4i* colv = reinterpret_cast<const v4i*>(itp->cols);
+  const v4i cq0 = colv[0], cq1 = colv[1], cq2 = colv[2], cq3 = colv[3];
+  __builtin_amdgcn_sched_barrier(0);
+  const int row = itp->row, begin = itp->begin, end = itp->end, split_tile = itp->tile;
+  const int nt = end - begin;
+  const int cg = panel * kWaves + wave;
+  const int col = cg * kTile + j;  // this lane's output column
+  TRACE_POINT(0);
+
+  const Rsrc ra = make_rsrc(p.tiles), rbm = make_rsrc(p.b), rcol = make_rsrc(p.col_idx),
+             rsc = make_rsrc(p.a_scale);
+  // Per-lane parts of the operand offsets, fixed for the whole item.
+  const int voff_a = j * kTile + 16 * g;
+  int voff_b, voff_b_last = 0, kb_last = -1;
+  const int brow = 8 * wave + (lane >> 3);  // row-major: this lane's slab row
+  if constexpr (BCOL) {
+    const int cc = col < p.N ? col : 0;  // past N: any valid column, never stored
+    voff_b = (int)(cc * p.ldb) + 16 * g;
+  } else {
+    int cb = panel * kPanel + 16 * (lane & 7);
+    cb = cb < p.N ? cb : 0;  // past N: any valid 16 bytes, never stored
+    voff_b = (int)(brow * p.ldb) + cb;
+    if (p.K % kTile) {  // the last slab reads row K-1 in place of rows past K
+      kb_last = p.K / kTile;
+      voff_b_last = (int)(min(brow, p.K - kb_last * kTile - 1) * p.ldb) + cb;
+    }
+  }
+  const int b_kstride = BCOL ? kTile : kTile * (int)p.ldb;  // bytes per block column
+
+  // Epilogue inputs, issued before the tile loads (branch-free: a load under
+  // a branch would make the compiler's vmcnt waits conservative).
+  float sb, bias;
+  {
+    const float* sbp = p.b_scale_vec ? p.b_scale_vec : p.a_scale;
+    const float* bip = p.bias ? p.bias : p.a_scale;
+    const int cc = min(col, p.N - 1);
+    const float vs = sbp[p.b_scale_vec ? cc : 0];
+    const float vb = bip[p.bias ? cc : 0];
+    sb = p.b_scale_vec ? vs : p.b_scale;
+    bias = p.bias ? vb : 0.f;
+  }
+  int rb = 0, re = 0;
+  float row_scale = 0.f;  // row-mean: a_scale of the row's first 64 tiles, one per lane
+  if constexpr (EPI == VOID_EPI_ROW_MEAN) {
+    if (split_tile < 0) {
+      rb = begin;
+      re = end;
+    } else {
+      rb = p.row_ptr[row];
+      re = p.row_ptr[row + 1];
+    }
+    row_scale = p.per_tensor_a ? p.a_scale[0] : p.a_scale[re > rb ? rb + min(lane, re - rb - 1) : 0];
+  }
+
+  typename A::Reg acc = {};
+  int kbs[kCgBatch];
+  int colw = 0;      // lane i: block column of tile min(i, nt - 1)
+  float scw = 0.f;   // lane i: a_scale of that tile (per-block epilogues)
+  // Block columns of batch bb: batches 0 and 1 from the work item (-1 marks
+  // slots past the item's end; they re-read the first column), later ones
+  // from colw (slots past the end read tile nt - 1's column).
+  auto take_cols = [&](int bb) {
+#pragma unroll
+    for (int u = 0; u < kCgBatch; ++u) {
+      int kb;
+      if (bb < 2) {
+        const int c0 = u < 4 ? cq0[u & 3] : cq1[u & 3];
+        const int c1 = u < 4 ? cq2[u & 3] : cq3[u & 3];
+        kb = bb == 0 ? c0 : c1;
+        kb = kb >= 0 ? kb : max(cq0[0], 0);
+      } else {
+        kb = __builtin_amdgcn_readlane(colw, min(bb * kCgBatch + u, kCgMaxTiles - 1));
+      }
+      kbs[u] = __builtin_amdgcn_readfirstlane(kb);
+    }
+  };
+  auto issue = [&](CgBatch& x, int bb) {
+    const int base = bb * kCgBatch;
+#pragma unroll
+    for (int q = 0; q < kCgAPerWave; ++q) {
+      const int idx = base + wave + kWaves * q;
+      const int t = begin + (idx < nt ? idx : 0);  // past the end: re-read tile 'begin'
+      x.a[q] = __builtin_amdgcn_raw_buffer_load_b128(ra, voff_a, t * (kTile * kTile), 0);
+    }
+    int mask = 0;
+#pragma unroll
+    for (int u = 0; u < kCgBatch; ++u) {
+      int vo = voff_b;
+      if constexpr (!BCOL) {
+        const bool last = kbs[u] == kb_last;
+        mask |= (int)last << u;
+        vo = last ? voff_b_last : voff_b;
+      }
+      x.b[u] = __builtin_amdgcn_raw_buffer_load_b128(rbm, vo, kbs[u] * b_kstride, 0);
+    }
+    x.last_mask = mask;
+  };
+  auto consume = [&](const CgBatch& x, int bb) {
+    const int base = bb * kCgBatch;
+    const int buf = bb & 1;
+#pragma unroll
+    for (int q = 0; q < kCgAPerWave; ++q) a_lds[buf][wave + kWaves * q][lane] = x.a[q];
+    if constexpr (!BCOL) {
+#pragma unroll
+      for (int u = 0; u < kCgBatch; ++u) {
+        v4i v = x.b[u];
+        if constexpr (ELT == kEltFp8) {
+          // Rows past K in the slab that crosses K: fp8 codes there may be
+          // NaN, and NaN times the zero padding of A is still NaN.
+          if (((x.last_mask >> u) & 1) && brow >= p.K - kb_last * kTile) v = v4i{0, 0, 0, 0};
+        }
+        *reinterpret_cast<v4i*>(&b_lds[buf][u][brow * kPanel + (((lane & 7) ^ (brow & 7)) << 4)]) = v;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kCgBatch; ++u) {
+      if (base + u < nt) {
+        Frag1 f;
+        f.a = a_lds[buf][u][lane];
+        if constexpr (BCOL) f.b = x.b[u];
+        else f.b = read_tr(&b_lds[buf][u][0], wave, j, g);
+        float s = 0.f;
+        if constexpr (kScales) s = bcast(scw, base + u);
+        A::step(acc, f, s);
+      }
+    }
+  };
+
+  if (nt > 0) {
+    {
+      const int ci = begin + min(lane, nt - 1);
+      colw = __builtin_amdgcn_raw_buffer_load_b32(rcol, ci * 4, 0, 0);
+      if constexpr (kScales)
+        scw = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsc, p.per_tensor_a ? 0 : ci * 4, 0, 0));
+    }
+    CgBatch X, Y;
+    take_cols(0);
+    issue(X, 0);
+    TRACE_POINT(1);
+    int bb = 0;
+    // Unrolled by two so that the two batch buffers keep fixed registers;
+    // every issued load is unconditional within its branch, which keeps the
+    // compiler's vmcnt waits exact.
+    while (true) {
+      if ((bb + 1) * kCgBatch < nt) {
+        take_cols(bb + 1);
+        issue(Y, bb + 1);
+        consume(X, bb);
+        ++bb;
+        if ((bb + 1) * kCgBatch < nt) {
+          take_cols(bb + 1);
+          issue(X, bb + 1);
+          consume(Y, bb);
+          ++bb;
+          continue;
+        }
+        consume(Y, bb);
+        break;
+      }
+      consume(X, bb);
+      break;
+    }
+  }
+  TRACE_POINT(2);
+  TRACE_POINT(3);
+
+  // MFMA 32x32 result layout: lane (j, g), register r holds row
+  // 8 (r / 4) + 4 g + r % 4 of column j.
+  if (split_tile >= 0) {
+    // Split row: publish this chunk's partial block with agent-coherent (sc1)
+    // stores, count arrivals per (row, panel), and let the last chunk read
+    // every partial back with agent-coherent loads and reduce them in chunk
+    // order, so the result does not depend on timing.
+    const int nchunks = itp->nchunks, slot = itp->slot, chunk = itp->chunk;
+    constexpr size_t kBlock = (size_t)kTile * kTile;  // one wave's block
+    int* part = static_cast<int*>(p.partials);
+    const size_t mine = (((size_t)(slot + chunk) * p.n_panels + panel) * kWaves + wave) * kBlock + lane * 16;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int w = kInt ? (int)acc[r] : __float_as_int((float)acc[r]);
+      __hip_atomic_store(part + mine + r, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are acknowledged
+    __syncthreads();
+    unsigned* ctr = p.counters + (size_t)split_tile * p.n_panels + panel;
+    if (tid == 0) {
+      const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = (old == (unsigned)(nchunks - 1));
+    }
+    __syncthreads();
+    if (!s_last) {
+      TRACE_FLUSH();
+      return;
+    }
+    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    typename A::Reg sum = {};
+    for (int ch = 0; ch < nchunks; ++ch) {
+      const size_t off = (((size_t)(slot + ch) * p.n_panels + panel) * kWaves + wave) * kBlock + lane * 16;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int x = __hip_atomic_load(part + off + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (kInt) sum[r] += x;
+        else sum[r] += __int_as_float(x);
+      }
+    }
+    acc = sum;
+  }
+
+  float mul = 1.f;
+  if constexpr (EPI == VOID_EPI_ROW_MEAN) {
+    // int_quant.py:519-526: S = sum fl(s_a * s_b) in tile order over the
+    // whole block-row, then S / n.  The row's scales sit one per lane and
+    // are folded sequentially with readlane.
+    float S = 0.f;
+    for (int t0 = rb; t0 < re; t0 += 64) {
+      const int n = min(64, re - t0);
+      const float mine = t0 == rb ? row_scale
+                                  : (p.per_tensor_a ? p.a_scale[0] : p.a_scale[t0 + min(lane, n - 1)]);
+      for (int q = 0; q < n; ++q) S = __fadd_rn(S, __fmul_rn(bcast(mine, q), sb));
+    }
+    mul = (re > rb) ? __fdiv_rn(S, (float)(re - rb)) : 0.f;
+  } else if constexpr (EPI == VOID_EPI_PER_BLOCK) {
+    mul = sb;
+  }
+
+  constexpr int esz = (OUT == VOID_DT_F32 || OUT == VOID_DT_I32) ? 4 : 2;
+  const Rsrc rc = make_rsrc(p.c);
+  const int ldc = (int)p.ldc;
+  const int voff_c = ((4 * g) * ldc + col) * esz;
+  const int row0 = row * kTile;
+  const bool full = row0 + kTile <= p.M && cg * kTile + kTile <= p.N;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int rr = 8 * (r >> 2) + (r & 3);
+    const int soff = (row0 + rr) * ldc * esz;
+    float x;
+    if constexpr (EPI == VOID_EPI_ROW_MEAN) x = __fmul_rn((float)acc[r], mul);
+    else if constexpr (EPI == VOID_EPI_PER_BLOCK) x = __fmul_rn((float)acc[r], mul);
+    else x = 0.f;
+    if (p.bias) x = __fadd_rn(x, bias);
+    x = activate(x, p.activation);
+    if (full || (row0 + rr + 4 * g < p.M && col < p.N)) {
+      if constexpr (OUT == VOID_DT_F32) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(x), rc, voff_c, soff, 0);
+      } else if constexpr (OUT == VOID_DT_I32) {
+        __builtin_amdgcn_raw_buffer_store_b32((int)acc[r], rc, voff_c, soff, 0);
+      } else {
+        const uint32_t h = OUT == VOID_DT_BF16 ? f32_to_bf16_bits(x) : f32_to_f16_bits(x);
+        __builtin_amdgcn_raw_buffer_store_b16((unsigned short)h, rc, voff_c, soff, 0);
+      }
+    }
+  }
+  TRACE_POINT(4);
+  TRACE_FLUSH();
+}
+
+template <int ELT, int EPI, int OUT, bool BCOL>
+int launch_cg(const Params& p, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL((spmm_cg_kernel<ELT, EPI, OUT, BCOL>), dim3(grid), dim3(kThreads), 0, stream, p);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(VOID_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return VOID_OK;
+}
+
+
 // B layouts: column-major (direct 16-byte loads), row-major through LDS
 // (16-byte aligned rows), row-major with in-register transposes (4-byte
 // aligned rows), or bytewise (anything else).
@@ -860,6 +1228,51 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
   else
     layout = (c_ok && (bu % 4 == 0) && (d->ldb % 4 == 0)) ? kRowVec : kRowByte;
   const int grid = (int)grid64;
+
+  // The column-group kernel addresses every operand with 31-bit buffer
+  // offsets; larger operands and the other B layouts use spmm_bsr_kernel.
+  // VOID_AMD_KERNEL=bsr forces the latter (for comparisons).
+  const int esz = (d->out_dtype == VOID_DT_BF16 || d->out_dtype == VOID_DT_F16) ? 2 : 4;
+  const int64_t kLim = (int64_t)1 << 31;
+  const int64_t b_span = d->b_col_major ? (int64_t)d->N * d->ldb
+                                        : (int64_t)((a->K + kTile - 1) / kTile) * kTile * d->ldb;
+  const char* force = getenv("VOID_AMD_KERNEL");
+  const bool cg_ok = (layout == kRowLds || layout == kColVec) && plan->chunk_tiles <= kCgMaxTiles &&
+                     (int64_t)a->n_blocks * kTile * kTile < kLim &&
+                     b_span < kLim && (int64_t)a->M * d->ldc * esz < kLim &&
+                     !(force && strcmp(force, "bsr") == 0);
+  if (cg_ok) {
+    const bool bcol = layout == kColVec;
+    auto go = [&](auto elt_c, auto epi_c) -> int {
+      constexpr int E = decltype(elt_c)::value, P = decltype(epi_c)::value;
+      if constexpr (P == VOID_EPI_RAW_I32) {
+        return bcol ? launch_cg<E, P, VOID_DT_I32, true>(p, grid, stream)
+                    : launch_cg<E, P, VOID_DT_I32, false>(p, grid, stream);
+      } else {
+        switch (d->out_dtype) {
+          case VOID_DT_F32:
+            return bcol ? launch_cg<E, P, VOID_DT_F32, true>(p, grid, stream)
+                        : launch_cg<E, P, VOID_DT_F32, false>(p, grid, stream);
+          case VOID_DT_BF16:
+            return bcol ? launch_cg<E, P, VOID_DT_BF16, true>(p, grid, stream)
+                        : launch_cg<E, P, VOID_DT_BF16, false>(p, grid, stream);
+          case VOID_DT_F16:
+            return bcol ? launch_cg<E, P, VOID_DT_F16, true>(p, grid, stream)
+                        : launch_cg<E, P, VOID_DT_F16, false>(p, grid, stream);
+          default:
+            return fail(VOID_ERR_UNSUPPORTED, "out_dtype %d not supported with this epilogue", d->out_dtype);
+        }
+      }
+    };
+    using I8 = std::integral_constant<int, kEltI8>;
+    using F8 = std::integral_constant<int, kEltFp8>;
+    if (elt == kEltFp8) return go(F8{}, std::integral_constant<int, VOID_EPI_PER_BLOCK>{});
+    switch (epilogue) {
+      case VOID_EPI_RAW_I32: return go(I8{}, std::integral_constant<int, VOID_EPI_RAW_I32>{});
+      case VOID_EPI_ROW_MEAN: return go(I8{}, std::integral_constant<int, VOID_EPI_ROW_MEAN>{});
+      default: return go(I8{}, std::integral_constant<int, VOID_EPI_PER_BLOCK>{});
+    }
+  }
 
   if (elt == kEltI8) {
     switch (epilogue) {
