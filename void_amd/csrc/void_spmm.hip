@@ -782,10 +782,15 @@ static_assert(2 * kCgBatch <= kInline, "the first two batches' columns come from
 
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 
+// Raw buffers (stride 0) span 2^31 - 1 bytes; the host checks that every
+// operand's offsets fit in 31 bits.  A per-lane offset of kOutOfRange makes
+// a load return zeros without a memory request: slots past the end of an
+// item are filled that way, so that the number of issued loads (and so every
+// vmcnt wait) stays fixed.
+constexpr int kOutOfRange = (int)0x80000000u;
+
 __device__ __forceinline__ Rsrc make_rsrc(const void* p) {
-  // Raw buffer (stride 0) over the whole 32-bit offset range; the host
-  // checks that every operand's offsets fit in 31 bits.
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, -1, 0x00020000);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, 0x7fffffff, 0x00020000);
 }
 
 // One tile's MFMA operands for a single 32-column group.
@@ -936,8 +941,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int q = 0; q < kCgAPerWave; ++q) {
       const int idx = base + wave + kWaves * q;
-      const int t = begin + (idx < nt ? idx : 0);  // past the end: re-read tile 'begin'
-      x.a[q] = __builtin_amdgcn_raw_buffer_load_b128(ra, voff_a, t * (kTile * kTile), 0);
+      const bool live = idx < nt;
+      x.a[q] = __builtin_amdgcn_raw_buffer_load_b128(ra, live ? voff_a : kOutOfRange,
+                                                     (begin + (live ? idx : 0)) * (kTile * kTile), 0);
     }
     int mask = 0;
 #pragma unroll
@@ -948,7 +954,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         mask |= (int)last << u;
         vo = last ? voff_b_last : voff_b;
       }
-      x.b[u] = __builtin_amdgcn_raw_buffer_load_b128(rbm, vo, kbs[u] * b_kstride, 0);
+      x.b[u] = __builtin_amdgcn_raw_buffer_load_b128(rbm, base + u < nt ? vo : kOutOfRange, kbs[u] * b_kstride, 0);
     }
     x.last_mask = mask;
   };
