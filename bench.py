@@ -38,10 +38,11 @@ HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0   # dense MFMA int8, MI355X
 FP8_PEAK_TFLOPS = 5000.0  # dense MFMA fp8, MI355X
 
-# Per-launch HBM traffic of the dominant kernel measured with rocprofv3 --pmc
-# (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration); None
-# until measured for a workload.
-MEASURED_TRAFFIC = {}
+# Per-launch HBM traffic (bytes) of the SpMM measured with rocprofv3 --pmc
+# FETCH_SIZE and WRITE_SIZE in separate runs of `bench.py --counters`, each
+# scaled by what the same counter reads for a plain 64 MiB copy (FETCH x 1.9993,
+# WRITE x 1.0).  Workloads not listed here report null.
+MEASURED_TRAFFIC = {"c2": 19869763, "c3": 22554836, "c4": 110925403, "c5": 187509457}
 
 
 def parse():

@@ -246,3 +246,29 @@ def test_fp8_ragged_k(gpu, M, K, N, kernel):
     err = np.abs(got.astype(np.float64) - ref)
     bad = np.argwhere(err > FP8_TOL * bound + 1e-30)
     assert len(bad) == 0, [(tuple(i), got[tuple(i)], ref[tuple(i)], bound[tuple(i)]) for i in bad[:8]]
+
+
+@pytest.mark.parametrize("epilogue", [_lib.EPI_ROW_MEAN, _lib.EPI_PER_BLOCK])
+def test_abi_empty_matrix_null_pointers(gpu, epilogue, kernel):
+    # Straight through the C ABI: a matrix with no tiles may pass null tile,
+    # scale and column pointers; every output element is still written.
+    import ctypes
+    from void_amd import _runtime
+    M, K, N = 96, 64, 128
+    row_ptr = np.zeros(M // 32 + 1, np.int32)
+    items, n_tiles, n_slots = _runtime.plan_rows(row_ptr, 64, np.zeros(0, np.int32))
+    dev_items = torch.from_numpy(items).to(gpu)
+    rp = torch.from_numpy(row_ptr).to(gpu)
+    b = torch.zeros(K, N, dtype=torch.int8, device=gpu)
+    out = torch.full((M, N), float("nan"), device=gpu)
+    desc = _lib.BsrDesc(tiles=None, scales=None, row_ptr=rp.data_ptr(), col_idx=None, M=M, K=K, n_blocks=0,
+                        n_block_rows=M // 32, per_tensor_a=0, reserved=0)
+    dense = _lib.DenseArgs(b=b.data_ptr(), ldb=N, b_col_major=0, N=N, b_scale=1.0, b_scale_vec=None, bias=None,
+                           c=out.data_ptr(), ldc=N, out_dtype=_lib.DT_F32, activation=_lib.ACT_NONE)
+    plan = _lib.Plan(items=dev_items.data_ptr(), n_items=items.shape[0], n_split_tiles=0, n_slots=0,
+                     chunk_tiles=64)
+    st = _lib.lib().void_spmm_int8(ctypes.byref(desc), ctypes.byref(dense), epilogue, ctypes.byref(plan),
+                                   None, 0, torch.cuda.current_stream().cuda_stream)
+    assert st == 0, _lib.lib().void_last_error()
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out.nan_to_num(1.0)) == 0

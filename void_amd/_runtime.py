@@ -91,6 +91,12 @@ class DeviceBsr:
     n_block_rows: int
     plans: Dict[int, DevicePlan] = field(default_factory=dict)
 
+    @property
+    def max_row(self) -> int:
+        """Tiles in the longest block-row."""
+        rp = self.row_ptr_host
+        return int(np.max(np.diff(rp))) if len(rp) > 1 else 0
+
     def plan(self, chunk: int) -> DevicePlan:
         p = self.plans.get(chunk)
         if p is None:

@@ -481,7 +481,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int nt = end - begin;
   const int tl = begin + min(lane, max(nt - 1, 0));
   float my_scale = 0.f;
-  if constexpr (EPI == VOID_EPI_PER_BLOCK) my_scale = p.per_tensor_a ? p.a_scale[0] : p.a_scale[tl];
+  if constexpr (EPI == VOID_EPI_PER_BLOCK) {
+    const float* msp = nt > 0 ? p.a_scale : reinterpret_cast<const float*>(p.row_ptr);  // empty: a dummy read
+    my_scale = msp[nt > 0 && !p.per_tensor_a ? tl : 0];
+  }
   auto scale_of = [&](int idx) -> float {
     if constexpr (EPI != VOID_EPI_PER_BLOCK) return 0.f;
     if (idx < 64) return bcast(my_scale, idx);
@@ -536,8 +539,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // conservative): absent vectors read a_scale[0] and are then ignored.
   float sb[4], bias[4];
   {
-    const float* sbp = p.b_scale_vec ? p.b_scale_vec : p.a_scale;
-    const float* bip = p.bias ? p.bias : p.a_scale;
+    const float* sbp = p.b_scale_vec ? p.b_scale_vec : reinterpret_cast<const float*>(p.row_ptr);
+    const float* bip = p.bias ? p.bias : reinterpret_cast<const float*>(p.row_ptr);
     const int cmax = (p.b_scale_vec || p.bias) ? p.N - 1 : 0;
     float vs[4], vb[4];
 #pragma unroll
@@ -559,12 +562,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     if (split_tile < 0) {
       rb = begin;
       re = end;
-      row_scale = p.per_tensor_a ? p.a_scale[0] : p.a_scale[tl];
     } else {
       rb = p.row_ptr[row];
       re = p.row_ptr[row + 1];
-      row_scale = p.per_tensor_a ? p.a_scale[0] : p.a_scale[rb + min(lane, max(re - rb - 1, 0))];
     }
+    // An empty row reads row_ptr[0] (always present) and ignores it.
+    const float* rsp = re > rb ? p.a_scale : reinterpret_cast<const float*>(p.row_ptr);
+    row_scale = rsp[re > rb ? (p.per_tensor_a ? 0 : rb + min(lane, re - rb - 1)) : 0];
   }
 
   if (has_first) {
@@ -893,8 +897,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // a branch would make the compiler's vmcnt waits conservative).
   float sb, bias;
   {
-    const float* sbp = p.b_scale_vec ? p.b_scale_vec : p.a_scale;
-    const float* bip = p.bias ? p.bias : p.a_scale;
+    const float* sbp = p.b_scale_vec ? p.b_scale_vec : reinterpret_cast<const float*>(p.row_ptr);
+    const float* bip = p.bias ? p.bias : reinterpret_cast<const float*>(p.row_ptr);
     const int cc = min(col, p.N - 1);
     const float vs = sbp[p.b_scale_vec ? cc : 0];
     const float vb = bip[p.bias ? cc : 0];
@@ -911,7 +915,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       rb = p.row_ptr[row];
       re = p.row_ptr[row + 1];
     }
-    row_scale = p.per_tensor_a ? p.a_scale[0] : p.a_scale[re > rb ? rb + min(lane, re - rb - 1) : 0];
+    // An empty row reads row_ptr[0] (always present) and ignores it.
+    const float* rsp = re > rb ? p.a_scale : reinterpret_cast<const float*>(p.row_ptr);
+    row_scale = rsp[re > rb ? (p.per_tensor_a ? 0 : rb + min(lane, re - rb - 1)) : 0];
   }
 
   typename A::Reg acc = {};

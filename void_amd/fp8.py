@@ -244,7 +244,7 @@ def void_spmm_fp8(a: FP8VOIDTensor, b: torch.Tensor, output_dtype: torch.dtype =
     from .fusion import get_activation_code
     if bias is not None:
         bias = bias.to(device=b.device, dtype=torch.float32).contiguous()
-    chunk = chunk_tiles or tuning.select_chunk("fp8", a.n_blocks, N)
+    chunk = chunk_tiles or tuning.select_chunk("fp8", a.n_blocks, N, a.device_bsr().max_row)
     return _runtime.launch("fp8", a.device_bsr(), b.view(torch.uint8) if b.dim() == 2 else b,
                            b_scale=scalar_scale, b_scale_vec=scale_vec, out=out,
                            epilogue=_lib.EPI_PER_BLOCK, activation=get_activation_code(activation),

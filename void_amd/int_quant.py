@@ -370,7 +370,7 @@ def void_spmm_int8(
         raise ValueError(f"A on {a.values.device}, B on {b.device}")
     from .fusion import get_activation_code
     dbsr = a.device_bsr()
-    chunk = chunk_tiles or tuning.select_chunk("int8", a.n_blocks, N)
+    chunk = chunk_tiles or tuning.select_chunk("int8", a.n_blocks, N, a.device_bsr().max_row)
     if bias is not None:
         if bias.shape != (N,):
             raise ValueError(f"bias must be [{N}]")
