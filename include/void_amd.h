@@ -166,6 +166,25 @@ int void_spmm_int8(const void_bsr_desc* a, const void_dense_args* d, int32_t epi
 int void_spmm_fp8(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
                   void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* ---- Quantisers on the path's input side (one wave per tile) ---------- */
+
+/* Per-tile symmetric INT8 of n_tiles fp32 32x32 tiles (tile t at
+ * tiles[1024 t], row-major): s_t = max(max|x| / 128, 1e-8),
+ * q = clamp(round_half_even(x / s_t), -128, 127), bit-identical to the
+ * reference's per-block loop (void/int_quant.py:178-214, 254-305, 363-369
+ * under quantize_void_tensor, :328-388).  tiles and q 16-byte aligned;
+ * q[1024 n_tiles], scales[n_tiles]. */
+int void_quantize_tiles_i8(const float* tiles, int32_t n_tiles, int8_t* q, float* scales, hipStream_t stream);
+
+/* Per-tile E4M3FN with the reference's first-call scaling: s_t =
+ * max(max|x| / 448, 1e-12), code = e4m3_rne(clamp(x * (1 / s_t), +-448)),
+ * bit-identical to void/fp8.py:81-105 and 185-229 as used by
+ * void_tensor_to_fp8 (:749-766, per_block).  Same layout as above; amax
+ * (nullable, n_tiles floats) receives max|x| of every tile, the value the
+ * reference records in its amax history. */
+int void_quantize_tiles_fp8(const float* tiles, int32_t n_tiles, uint8_t* q, float* scales, float* amax,
+                            hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -202,3 +202,13 @@ def test_chunk_table():
     assert tuning.select_chunk("int8", 1638, 512) == 64                       # c2: no split
     assert tuning.select_chunk("int8", 17960, 256) == 64                      # c4: capped at 64
     assert tuning.n_panels(512) == 4 and tuning.n_panels(130) == 2
+
+
+def test_quantiser_argument_checks():
+    lib = _lib.lib()
+    assert lib.void_quantize_tiles_i8(None, 0, None, None, None) == 0          # nothing to do
+    assert lib.void_quantize_tiles_i8(None, -1, None, None, None) == -1
+    assert lib.void_quantize_tiles_i8(None, 3, None, None, None) == -1
+    assert b"null" in lib.void_last_error()
+    assert lib.void_quantize_tiles_fp8(0x1008, 3, 0x1000, 0x1000, None, None) == -1  # misaligned tiles
+    assert b"aligned" in lib.void_last_error()

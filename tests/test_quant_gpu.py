@@ -1,0 +1,79 @@
+"""Device-side tile quantisers (void_quantize_tiles_i8 / _fp8) against the
+oracle and the host path, bit for bit, including the rounding edge cases:
+ties to even, saturation at +-amax, all-zero tiles, E4M3 subnormals and
+midpoints, and the largest finite E4M3 value."""
+
+import numpy as np
+import pytest
+import torch
+
+import cases
+import oracle
+import void_amd
+from void_amd import _runtime
+
+pytestmark = pytest.mark.gpu
+
+
+def _edge_tiles(rng):
+    n = 48
+    t = rng.standard_normal((n, 32, 32)).astype(np.float32)
+    t[0] = 0.0                                          # scale floor (1e-8 / 1e-12)
+    t[1] *= 1e-30                                       # tiny amax
+    t[2, 0, 0] = 1e6                                    # one huge entry
+    t[3] = np.abs(t[3])                                 # all positive
+    t[4] = -np.abs(t[4])                                # all negative: -amax -> -128
+    # INT8 ties: amax 128 -> s = 1 exactly; x = k + 0.5 must round to even.
+    t[5] = (np.arange(1024).reshape(32, 32) % 255 - 127).astype(np.float32) + 0.5
+    t[5, 0, 0] = 128.0
+    # E4M3 with amax 448 -> scale 1 exactly: every code's midpoints and subnormals.
+    tab = oracle.e4m3_table()[:127].astype(np.float64)
+    mids = ((tab[:-1] + tab[1:]) / 2).astype(np.float32)
+    vals = np.concatenate([tab.astype(np.float32), mids, -mids, np.float32([2.0 ** -10, 2.0 ** -9 * 1.5, 447.9])])
+    t[6].reshape(-1)[:len(vals)] = vals
+    t[6, 31, 31] = 448.0
+    t[7] *= 1e-3                                        # many values in the E4M3 subnormal range after scaling
+    t[8, :, :16] = 0.0
+    return t
+
+
+def test_device_int8_tiles_bit_exact(gpu):
+    tiles = _edge_tiles(np.random.default_rng(0))
+    q, s = _runtime.quantize_tiles_i8(torch.from_numpy(tiles).to(gpu))
+    oq, os_ = oracle.quantize_i8_blocks(tiles)
+    assert np.array_equal(q.cpu().numpy(), oq)
+    assert np.array_equal(s.cpu().numpy().view(np.int32), os_.view(np.int32))
+
+
+def test_device_fp8_tiles_bit_exact(gpu):
+    tiles = _edge_tiles(np.random.default_rng(1))
+    x = torch.from_numpy(tiles).to(gpu)
+    q, s, amax = _runtime.quantize_tiles_fp8(x)
+    oq, os_ = oracle.quantize_fp8_blocks(tiles)
+    assert np.array_equal(q.cpu().numpy(), oq)
+    assert np.array_equal(s.cpu().numpy().view(np.int32), os_.view(np.int32))
+    assert np.array_equal(amax.cpu().numpy(), np.abs(tiles).reshape(len(tiles), -1).max(axis=1))
+    # and against torch's own cast on the GPU (the reference's quantize_to_fp8 arithmetic)
+    inv = 1.0 / s
+    ref = torch.clamp(x * inv.view(-1, 1, 1), -448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8)
+    assert torch.equal(q, ref)
+
+
+def test_public_api_device_matches_host(gpu):
+    case = cases.uniform_blocks(1024, 2048, 64, 700, seed=12)
+    vt = cases.make_void_tensor(case, "cpu")
+    host = void_amd.quantize_void_tensor(vt)
+    dev = void_amd.quantize_void_tensor(vt.to(gpu))
+    assert dev.values.is_cuda
+    assert torch.equal(dev.values.cpu(), host.values) and torch.equal(dev.scales.cpu(), host.scales)
+    f_host = void_amd.void_tensor_to_fp8(vt)
+    f_dev = void_amd.void_tensor_to_fp8(vt.to(gpu))
+    assert torch.equal(f_dev.values_fp8.view(torch.uint8).cpu(), f_host.values_fp8.view(torch.uint8))
+    for name in ("scale", "scale_inv", "amax"):
+        assert torch.equal(getattr(f_dev.scaling_info, name).cpu(), getattr(f_host.scaling_info, name)), name
+    # The device-quantised operands feed the SpMM unchanged.
+    bq, bs = oracle.quantize_i8_columns(case.b)
+    out = void_amd.void_spmm_int8(dev, torch.from_numpy(bq).to(gpu), b_scale=torch.from_numpy(bs).to(gpu),
+                                  epilogue="raw_i32")
+    A = oracle.Bsr(host.values.numpy(), host.scales.numpy(), case.block_rows, case.block_cols, (case.M, case.K))
+    assert np.array_equal(out.cpu().numpy(), oracle.i8_acc(A, bq))

@@ -196,3 +196,32 @@ def out_code(dtype: torch.dtype) -> int:
     if dtype not in _OUT_CODES:
         raise ValueError(f"unsupported output dtype {dtype}")
     return _OUT_CODES[dtype]
+
+
+def device_tile_quant_ok(values: torch.Tensor) -> bool:
+    """The device quantisers take contiguous fp32 [n, 32, 32] GPU tiles."""
+    return (values.is_cuda and values.dtype == torch.float32 and values.dim() == 3
+            and tuple(values.shape[1:]) == (32, 32) and values.is_contiguous() and values.shape[0] > 0)
+
+
+def quantize_tiles_i8(values: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(codes int8 [n,32,32], scales f32 [n]) from the gfx950 per-tile INT8 quantiser."""
+    n = values.shape[0]
+    q = torch.empty(values.shape, dtype=torch.int8, device=values.device)
+    scales = torch.empty(n, dtype=torch.float32, device=values.device)
+    st = _lib.lib().void_quantize_tiles_i8(values.data_ptr(), n, q.data_ptr(), scales.data_ptr(),
+                                           torch.cuda.current_stream(values.device).cuda_stream)
+    _lib.check(st, "void_quantize_tiles_i8")
+    return q, scales
+
+
+def quantize_tiles_fp8(values: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(codes uint8 [n,32,32], scales f32 [n], amax f32 [n]) from the gfx950 per-tile E4M3 quantiser."""
+    n = values.shape[0]
+    q = torch.empty(values.shape, dtype=torch.uint8, device=values.device)
+    scales = torch.empty(n, dtype=torch.float32, device=values.device)
+    amax = torch.empty(n, dtype=torch.float32, device=values.device)
+    st = _lib.lib().void_quantize_tiles_fp8(values.data_ptr(), n, q.data_ptr(), scales.data_ptr(),
+                                            amax.data_ptr(), torch.cuda.current_stream(values.device).cuda_stream)
+    _lib.check(st, "void_quantize_tiles_fp8")
+    return q, scales, amax

@@ -1,0 +1,168 @@
+// void_quant.hip — gfx950 kernels for the quantisers on the SpMM path's
+// input side: per-tile symmetric INT8 (quantize_void_tensor) and per-tile
+// E4M3 (void_tensor_to_fp8), declared in include/void_amd.h.
+//
+// One wave64 per 32x32 fp32 tile: each lane loads 16 consecutive values (four
+// 16-byte loads, so one tile is one contiguous 4 KB read), the wave reduces
+// the tile's amax with cross-lane max, and every lane writes its 16 codes as
+// one 16-byte store.  The work is HBM-bound byte traffic: 4 KB in, 1 KB + 4
+// bytes out per tile.  Rounding follows the reference's torch arithmetic
+// exactly: IEEE fp32 division and multiplication, round half to even.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "void_amd.h"
+
+extern "C" __attribute__((visibility("hidden"))) int void_internal_fail(int code, const char* msg);
+
+namespace {
+
+constexpr int kTileElems = 32 * 32;
+constexpr int kWavesPerBlock = 4;
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Loads this lane's 16 values of tile t and returns the tile's amax
+// (max |x|, which equals max(|min|, |max|) for finite values).
+__device__ __forceinline__ float load_tile(const float* tiles, int64_t t, int lane, float (&x)[16]) {
+  const v4f* p = reinterpret_cast<const v4f*>(tiles + t * kTileElems) + lane * 4;
+  float m = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const v4f v = p[q];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[4 * q + i] = v[i];
+      m = fmaxf(m, fabsf(v[i]));
+    }
+  }
+  return wave_max(m);
+}
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+         ((uint32_t)(d & 0xff) << 24);
+}
+
+// int_quant.py:178-214 (symmetric min/max scale), :254-305 (quantize_tensor):
+// s = max(amax / 128, 1e-8); q = clamp(round_half_even(x / s), -128, 127).
+__global__ __launch_bounds__(64 * kWavesPerBlock) void quantize_i8_kernel(const float* __restrict__ tiles,
+                                                                          int n_tiles, int8_t* __restrict__ q,
+                                                                          float* __restrict__ scales) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (t >= n_tiles) return;
+  float x[16];
+  const float amax = load_tile(tiles, t, lane, x);
+  const float s = fmaxf(__fdiv_rn(amax, 128.0f), 1e-8f);
+  int c[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) c[i] = (int)fminf(fmaxf(rintf(__fdiv_rn(x[i], s)), -128.0f), 127.0f);
+  v4i out;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) out[w] = (int)pack4(c[4 * w], c[4 * w + 1], c[4 * w + 2], c[4 * w + 3]);
+  *reinterpret_cast<v4i*>(q + t * kTileElems + lane * 16) = out;
+  if (lane == 0) scales[t] = s;
+}
+
+// E4M3FN code of a finite float32 in [-448, 448], round to nearest even.
+// Normal range (|x| >= 2^-6): keep 3 mantissa bits with RNE on the fp32
+// mantissa; a carry out of the mantissa bumps the exponent.  Subnormal range:
+// the code is round_half_even(|x| * 2^9) (exact scaling by a power of two),
+// which also yields the smallest normal (code 8) when it rounds up to 2^-6.
+__device__ __forceinline__ uint32_t e4m3_code(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const float a = fabsf(x);
+  uint32_t code;
+  if (a < 0.015625f) {
+    code = (uint32_t)rintf(a * 512.0f);
+  } else {
+    const uint32_t ua = u & 0x7fffffffu;
+    const int e = (int)(ua >> 23) - 127;  // -6 .. 8
+    const uint32_t m = ua & 0x7fffffu;
+    uint32_t m3 = (m + 0x7ffffu + ((m >> 20) & 1u)) >> 20;  // RNE to 3 bits, may reach 8
+    int ee = e + 7;
+    if (m3 == 8u) {
+      m3 = 0u;
+      ee += 1;
+    }
+    code = ((uint32_t)ee << 3) | m3;
+  }
+  return sign | code;
+}
+
+// fp8.py:81-105 (first-call scale from a zero amax history: amax / 448,
+// clamp 1e-12), :185-229 (x * (1 / scale), clamp to +-448, cast to E4M3FN).
+__global__ __launch_bounds__(64 * kWavesPerBlock) void quantize_fp8_kernel(const float* __restrict__ tiles,
+                                                                           int n_tiles, uint8_t* __restrict__ q,
+                                                                           float* __restrict__ scales,
+                                                                           float* __restrict__ amaxes) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  if (t >= n_tiles) return;
+  float x[16];
+  const float amax = load_tile(tiles, t, lane, x);
+  const float s = fmaxf(__fdiv_rn(amax, 448.0f), 1e-12f);
+  const float inv = __fdiv_rn(1.0f, s);
+  uint32_t c[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) c[i] = e4m3_code(fminf(fmaxf(__fmul_rn(x[i], inv), -448.0f), 448.0f));
+  v4i out;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) out[w] = (int)pack4(c[4 * w], c[4 * w + 1], c[4 * w + 2], c[4 * w + 3]);
+  *reinterpret_cast<v4i*>(q + t * kTileElems + lane * 16) = out;
+  if (lane == 0) {
+    scales[t] = s;
+    if (amaxes) amaxes[t] = amax;
+  }
+}
+
+int check_args(const float* tiles, int32_t n_tiles, const void* q, const float* scales) {
+  if (n_tiles < 0) return void_internal_fail(VOID_ERR_ARG, "negative tile count");
+  if (n_tiles == 0) return VOID_OK;
+  if (!tiles || !q || !scales) return void_internal_fail(VOID_ERR_ARG, "null tile, code or scale pointer");
+  if ((uintptr_t)tiles % 16 || (uintptr_t)q % 16)
+    return void_internal_fail(VOID_ERR_ARG, "tiles and codes must be 16-byte aligned");
+  return 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int void_quantize_tiles_i8(const float* tiles, int32_t n_tiles, int8_t* q, float* scales, hipStream_t stream) {
+  void_internal_fail(VOID_OK, "");
+  const int st = check_args(tiles, n_tiles, q, scales);
+  if (st <= 0) return st;
+  const int grid = (n_tiles + kWavesPerBlock - 1) / kWavesPerBlock;
+  hipLaunchKernelGGL(quantize_i8_kernel, dim3(grid), dim3(64 * kWavesPerBlock), 0, stream, tiles, n_tiles, q,
+                     scales);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return void_internal_fail(VOID_ERR_HIP, hipGetErrorString(e));
+  return VOID_OK;
+}
+
+int void_quantize_tiles_fp8(const float* tiles, int32_t n_tiles, uint8_t* q, float* scales, float* amax,
+                            hipStream_t stream) {
+  void_internal_fail(VOID_OK, "");
+  const int st = check_args(tiles, n_tiles, q, scales);
+  if (st <= 0) return st;
+  const int grid = (n_tiles + kWavesPerBlock - 1) / kWavesPerBlock;
+  hipLaunchKernelGGL(quantize_fp8_kernel, dim3(grid), dim3(64 * kWavesPerBlock), 0, stream, tiles, n_tiles, q,
+                     scales, amax);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return void_internal_fail(VOID_ERR_HIP, hipGetErrorString(e));
+  return VOID_OK;
+}
+
+}  // extern "C"

@@ -750,6 +750,15 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+}  // namespace
+
+// Error reporting for the library's other translation units.
+extern "C" __attribute__((visibility("hidden"))) int void_internal_fail(int code, const char* msg) {
+  return fail(code, "%s", msg);
+}
+
+namespace {
+
 template <int ELT, int EPI, int OUT, bool BCOL, bool VEC, bool LDSB = false>
 int launch(const Params& p, int grid, hipStream_t stream) {
   hipLaunchKernelGGL((spmm_bsr_kernel<ELT, EPI, OUT, BCOL, VEC, LDSB>), dim3(grid), dim3(kThreads), 0, stream, p);

@@ -145,7 +145,22 @@ class FP8VOIDTensor:
     @classmethod
     def from_void_tensor(cls, void_tensor, config: Optional[FP8Config] = None) -> "FP8VOIDTensor":
         config = config or FP8Config(scale_mode="per_block")
-        values_fp8, info = quantize_to_fp8(void_tensor.values, config=config)
+        if (config.format == FP8Format.E4M3 and config.scale_mode == "per_block" and config.margin == 0.0
+                and _runtime.device_tile_quant_ok(void_tensor.values)):
+            # GPU tiles: the gfx950 quantiser (void_quantize_tiles_fp8).  Its
+            # scale is the true fp32 quotient amax / 448, as the reference
+            # computes on the CPU; torch on a GPU divides a tensor by a Python
+            # scalar as a multiplication by the reciprocal, which can differ in
+            # the last bit, so the scale is taken from the kernel, not from
+            # compute_scale().
+            codes, scale, amax = _runtime.quantize_tiles_fp8(void_tensor.values)
+            info = create_scaling_info(void_tensor.values.shape, config, void_tensor.values.device)
+            info.update_amax(amax)
+            info.scale = scale
+            info.scale_inv = 1.0 / scale
+            values_fp8 = codes.view(config.torch_dtype)
+        else:
+            values_fp8, info = quantize_to_fp8(void_tensor.values, config=config)
         return cls(values_fp8=values_fp8, scaling_info=info, block_rows=void_tensor.block_rows,
                    block_cols=void_tensor.block_cols, morton_codes=void_tensor.morton_codes,
                    shape=void_tensor.shape, tile_size=void_tensor.tile_size,

@@ -251,7 +251,12 @@ def quantize_void_tensor(void_tensor, config: Optional[IntQuantConfig] = None) -
     if config.scale_mode == ScaleMode.PER_BLOCK:
         if config.calibration_method != "minmax":
             raise ValueError(f"per-block quantisation uses minmax calibration, got {config.calibration_method}")
-        if n_blocks:
+        if (config.format == IntFormat.INT8 and config.symmetric
+                and _runtime.device_tile_quant_ok(values)):
+            # GPU tiles: the gfx950 quantiser (void_quantize_tiles_i8), same arithmetic.
+            q, scales = _runtime.quantize_tiles_i8(values)
+            zero_points = torch.zeros(n_blocks, dtype=torch.int8, device=values.device)
+        elif n_blocks:
             scale, zp = compute_scale_minmax(values, config, dim=(1, 2))
             q = _apply_quant(values, scale, zp, config)
             scales = scale.reshape(n_blocks).to(torch.float32)
