@@ -51,6 +51,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--op", default="spmm", choices=["spmm", "quantize", "format"],
+                    help="spmm (default): the SpMM; quantize: device per-tile INT8 quantisation of the config's "
+                         "A tiles; format: device CSR -> VOID tiles of the config's A")
     ap.add_argument("--epilogue", default=None, help="int8 epilogue (default per_block)")
     ap.add_argument("--chunk", type=int, default=None, help="override the Stream-K chunk")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
@@ -197,6 +200,93 @@ def run_for_counters(prob, steps: int):
     torch.cuda.synchronize()
 
 
+def bench_input_side(args, dev):
+    """The device quantiser or the device CSR -> tiles conversion on the A
+    operand of a config, timed like the SpMM (cold: after a 1 GiB overwrite),
+    with the host path on the same input as the CPU baseline."""
+    import scipy.sparse as sp
+    import torch
+
+    import cases
+    import void_amd
+    from void_amd import _lib, _runtime
+    case = {"c1": None, "c2": cases.c2_int8, "c3": cases.c3_fp8, "c4": cases.c4_powerlaw, "c5": cases.c5_ffn}[args.config]
+    if case is None:
+        A, _ = cases.c1_plumbing()
+        vt_host = void_amd.csr_to_void(A)
+        name = "c1_plumbing_512_n128"
+    else:
+        case = case()
+        vt_host = cases.make_void_tensor(case, "cpu")
+        name = case.name
+    nb = vt_host.n_blocks
+    M, K = vt_host.shape
+    if args.op == "quantize":
+        x = vt_host.values.to(dev)
+        run = lambda: _runtime.quantize_tiles_i8(x)
+        nbytes = nb * (4096 + 1024 + 4)
+        host = lambda: void_amd.quantize_void_tensor(vt_host)
+        metric = f"INT8 per-tile quantisation GB/s, A tiles of {name}"
+        sample = f"quantize_void_tensor on the host (batched torch CPU), all {nb} tiles"
+    else:
+        dense = vt_host.to_dense().numpy()
+        A = sp.csr_matrix(dense)
+        nnz = A.nnz
+        lib = _lib.lib()
+        ws_bytes = lib.void_csr_workspace_bytes(M, K)
+        d_indptr = torch.from_numpy(A.indptr.astype(np.int32)).to(dev)
+        d_indices = torch.from_numpy(A.indices.astype(np.int32)).to(dev)
+        d_data = torch.from_numpy(A.data.astype(np.float32)).to(dev)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        cnt = torch.empty(1, dtype=torch.int64, device=dev)
+        values = torch.empty((nb, 32, 32), dtype=torch.float32, device=dev)
+        rows = torch.empty(nb, dtype=torch.int32, device=dev)
+        cols = torch.empty(nb, dtype=torch.int32, device=dev)
+        mort = torch.empty(nb, dtype=torch.int64, device=dev)
+
+        def run():
+            st = torch.cuda.current_stream().cuda_stream
+            _lib.check(lib.void_csr_count_blocks(d_indptr.data_ptr(), d_indices.data_ptr(), M, K, ws.data_ptr(),
+                                                 ws_bytes, cnt.data_ptr(), st), "count")
+            _lib.check(lib.void_csr_to_tiles(d_indptr.data_ptr(), d_indices.data_ptr(), d_data.data_ptr(), M, K,
+                                             ws.data_ptr(), ws_bytes, nb, values.data_ptr(), rows.data_ptr(),
+                                             cols.data_ptr(), mort.data_ptr(), st), "to_tiles")
+        run()
+        torch.cuda.synchronize()
+        assert int(cnt.item()) == nb and torch.equal(values.cpu(), vt_host.values)
+        nbytes = 4 * (M + 1) + 8 * nnz + nb * (4096 + 16)
+        host = lambda: void_amd.csr_to_void(A)
+        metric = f"CSR -> VOID tiles GB/s (device csr_to_void), A of {name}"
+        sample = f"csr_to_void on the host (vectorised numpy scatter), nnz {nnz}"
+    cold, hot, wall = time_gpu({"run": run}, args.steps, args.warmup, flush=True)
+    gbs = nbytes / (cold * 1e-3) / 1e9
+    cpu = None
+    if args.cpu_seconds > 0:
+        t_end = time.perf_counter() + args.cpu_seconds
+        times = []
+        while True:
+            t = time.perf_counter()
+            host()
+            times.append(time.perf_counter() - t)
+            if time.perf_counter() > t_end and len(times) >= 3:
+                break
+        med = statistics.median(times[1:]) if len(times) > 1 else times[0]
+        cpu = {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": len(os.sched_getaffinity(0)),
+               "kind": "port", "ms": round(med * 1e3, 3), "sample": sample + f", median of {len(times) - 1} reps"}
+    line = {"metric": metric, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(cold, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32->int8" if args.op == "quantize" else "f32",
+            "data": "synthetic (seeded generators of BASELINE.json configs)",
+            "config": {"workload": name, "op": args.op, "n_tiles": nb, "M": M, "K": K,
+                       "cache": "cold (1 GiB overwrite between steps)"},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "algorithmic_bytes": nbytes},
+            "cpu_baseline": cpu,
+            "extra": {"hot_ms": round(hot, 5), "hot_gbs": round(nbytes / (hot * 1e-3) / 1e9, 1),
+                      "wall_s": round(wall, 3)}}
+    print(json.dumps(line), flush=True)
+
+
 def time_cpu(prob, budget_s: float):
     import torch
 
@@ -224,6 +314,9 @@ def main():
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
+    if args.op != "spmm":
+        bench_input_side(args, dev)
+        return
     prob = build_problem(args.config, dev, args.epilogue)
     if args.chunk:
         prob["chunk"] = args.chunk

@@ -185,6 +185,23 @@ int void_quantize_tiles_i8(const float* tiles, int32_t n_tiles, int8_t* q, float
 int void_quantize_tiles_fp8(const float* tiles, int32_t n_tiles, uint8_t* q, float* scales, float* amax,
                             hipStream_t stream);
 
+/* ---- CSR -> VOID tiles on the device (csr_to_void, void/format.py:248-349) --
+ * Canonical CSR (int32 indptr[M+1] and column indices, no duplicate
+ * entries; float32 values) becomes Morton-ordered 32x32 fp32 tiles, block
+ * rows, block columns and Morton codes, the reference's VOIDTensor fields.
+ * Explicit zeros activate their tile, as in the reference.  Two calls:
+ * void_csr_count_blocks writes the number of active blocks to *n_blocks (a
+ * device int64), the caller sizes the outputs from it, then
+ * void_csr_to_tiles fills them.  Both use the same workspace of
+ * void_csr_workspace_bytes(M, N) bytes (0 when the block grid is too large
+ * for the device conversion: more than 2^28 blocks). */
+size_t void_csr_workspace_bytes(int32_t M, int32_t N);
+int void_csr_count_blocks(const int32_t* indptr, const int32_t* indices, int32_t M, int32_t N, void* workspace,
+                          size_t workspace_bytes, int64_t* n_blocks, hipStream_t stream);
+int void_csr_to_tiles(const int32_t* indptr, const int32_t* indices, const float* data, int32_t M, int32_t N,
+                      void* workspace, size_t workspace_bytes, int64_t n_blocks, float* values,
+                      int32_t* block_rows, int32_t* block_cols, int64_t* morton, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

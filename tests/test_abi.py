@@ -212,3 +212,12 @@ def test_quantiser_argument_checks():
     assert b"null" in lib.void_last_error()
     assert lib.void_quantize_tiles_fp8(0x1008, 3, 0x1000, 0x1000, None, None) == -1  # misaligned tiles
     assert b"aligned" in lib.void_last_error()
+
+
+def test_csr_conversion_argument_checks():
+    lib = _lib.lib()
+    assert lib.void_csr_workspace_bytes(100, 100) > 0
+    assert lib.void_csr_workspace_bytes(2 ** 30, 2 ** 30) == 0          # block grid beyond the device limit
+    assert lib.void_csr_count_blocks(None, None, 10, 10, None, 0, None, None) == -1
+    assert lib.void_csr_to_tiles(None, None, None, 10, 10, None, 0, 0, None, None, None, None, None) == 0
+    assert lib.void_csr_to_tiles(None, None, None, 10, 10, None, 0, 1, None, None, None, None, None) == -1

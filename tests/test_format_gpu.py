@@ -1,0 +1,64 @@
+"""Device-side csr_to_void (void_csr_count_blocks / void_csr_to_tiles)
+against the host conversion, field by field and bit for bit."""
+
+import numpy as np
+import pytest
+import scipy.sparse as sp
+import torch
+
+import cases
+import void_amd
+
+pytestmark = pytest.mark.gpu
+
+
+def _same(dev_vt, host_vt):
+    assert dev_vt.values.is_cuda
+    assert dev_vt.n_blocks == host_vt.n_blocks and dev_vt.nnz_original == host_vt.nnz_original
+    assert dev_vt.shape == host_vt.shape and dev_vt.density == host_vt.density
+    for name in ("values", "block_rows", "block_cols", "morton_codes"):
+        a, b = getattr(dev_vt, name).cpu(), getattr(host_vt, name)
+        assert a.dtype == b.dtype, name
+        assert torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("M,N,density,seed", [(300, 200, 0.05, 1), (2000, 70, 0.02, 2), (70, 3000, 0.02, 3),
+                                              (4096, 4096, 0.002, 4), (33, 33, 0.5, 5), (1, 1000, 0.1, 6)])
+def test_device_csr_to_void_matches_host(gpu, M, N, density, seed):
+    A = sp.random(M, N, density=density, format="csr", random_state=seed, dtype=np.float64)
+    A.sort_indices()
+    _same(void_amd.csr_to_void(A, device="cuda"), void_amd.csr_to_void(A))
+
+
+def test_device_csr_c1_and_explicit_zeros(gpu):
+    A, _ = cases.c1_plumbing()
+    _same(void_amd.csr_to_void(A, device="cuda"), void_amd.csr_to_void(A))
+    # Explicit zeros activate their tiles (format.py:321-327 stores them).
+    z = sp.csr_matrix((np.array([0.0, 2.0, 0.0]), (np.array([5, 40, 99]), np.array([7, 70, 1]))), shape=(100, 100))
+    dev = void_amd.csr_to_void(z, device="cuda")
+    _same(dev, void_amd.csr_to_void(z))
+    assert dev.n_blocks == 3
+
+
+def test_device_csr_empty_and_duplicates(gpu):
+    e = sp.csr_matrix((100, 64), dtype=np.float32)
+    dev = void_amd.csr_to_void(e, device="cuda")
+    assert dev.n_blocks == 0 and dev.values.shape == (0, 32, 32)
+    # Duplicate entries (non-canonical CSR) keep the host rule: the last one wins.
+    d = sp.csr_matrix((np.array([1.0, 5.0, 3.0]), np.array([4, 4, 9]), np.array([0, 3, 3])), shape=(2, 40))
+    assert not d.has_canonical_format
+    vt = void_amd.csr_to_void(d, device="cuda")
+    assert vt.values.is_cuda and vt.to_dense()[0, 4].item() == 5.0
+
+
+def test_device_format_feeds_the_spmm(gpu):
+    case = cases.c2_int8()
+    dense = np.zeros((case.M, case.K), np.float32)
+    for t in range(len(case.block_rows)):
+        r, c = case.block_rows[t] * 32, case.block_cols[t] * 32
+        dense[r:r + 32, c:c + 32] = case.tiles[t]
+    A = sp.csr_matrix(dense)
+    vt_dev = void_amd.csr_to_void(A, device="cuda")
+    q_dev = void_amd.quantize_void_tensor(vt_dev)
+    q_host = void_amd.quantize_void_tensor(void_amd.csr_to_void(A))
+    assert torch.equal(q_dev.values.cpu(), q_host.values) and torch.equal(q_dev.scales.cpu(), q_host.scales)

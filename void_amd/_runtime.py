@@ -225,3 +225,36 @@ def quantize_tiles_fp8(values: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor
                                             amax.data_ptr(), torch.cuda.current_stream(values.device).cuda_stream)
     _lib.check(st, "void_quantize_tiles_fp8")
     return q, scales, amax
+
+
+def csr_to_tiles(indptr: np.ndarray, indices: np.ndarray, data: np.ndarray, shape: Tuple[int, int],
+                 device: torch.device):
+    """Device CSR -> VOID tiles (void_csr_count_blocks + void_csr_to_tiles).
+
+    Returns (values f32 [n,32,32], block_rows i32, block_cols i32, morton i64)
+    in Morton order, or None when the block grid is too large for the device
+    conversion.  The CSR arrays must be canonical (no duplicate entries)."""
+    M, N = shape
+    lib = _lib.lib()
+    ws_bytes = lib.void_csr_workspace_bytes(M, N)
+    if ws_bytes == 0:
+        return None
+    stream = torch.cuda.current_stream(device).cuda_stream
+    d_indptr = torch.from_numpy(np.ascontiguousarray(indptr, dtype=np.int32)).to(device)
+    d_indices = torch.from_numpy(np.ascontiguousarray(indices, dtype=np.int32)).to(device)
+    d_data = torch.from_numpy(np.ascontiguousarray(data, dtype=np.float32)).to(device)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    count = torch.empty(1, dtype=torch.int64, device=device)
+    idx_ptr = d_indices.data_ptr() if d_indices.numel() else d_indptr.data_ptr()
+    _lib.check(lib.void_csr_count_blocks(d_indptr.data_ptr(), idx_ptr, M, N, ws.data_ptr(), ws_bytes,
+                                         count.data_ptr(), stream), "void_csr_count_blocks")
+    n = int(count.item())
+    values = torch.empty((n, 32, 32), dtype=torch.float32, device=device)
+    rows = torch.empty(n, dtype=torch.int32, device=device)
+    cols = torch.empty(n, dtype=torch.int32, device=device)
+    morton = torch.empty(n, dtype=torch.int64, device=device)
+    if n:
+        _lib.check(lib.void_csr_to_tiles(d_indptr.data_ptr(), d_indices.data_ptr(), d_data.data_ptr(), M, N,
+                                         ws.data_ptr(), ws_bytes, n, values.data_ptr(), rows.data_ptr(),
+                                         cols.data_ptr(), morton.data_ptr(), stream), "void_csr_to_tiles")
+    return values, rows, cols, morton

@@ -220,6 +220,23 @@ def csr_to_void(
     n_br = (M + tile_size - 1) // tile_size
     n_bc = (N + tile_size - 1) // tile_size
 
+    dev = torch.device(device)
+    if (dev.type == "cuda" and tile_size == 32 and matrix.has_canonical_format and nnz < 2 ** 31
+            and M < 2 ** 31 and N < 2 ** 31):
+        # Device conversion (void_csr_count_blocks / void_csr_to_tiles): same
+        # tiles, order and metadata.  Inputs with duplicate entries stay on
+        # the host path below, whose "last entry wins" rule needs the
+        # sequential order.
+        from . import _runtime
+        built = _runtime.csr_to_tiles(matrix.indptr, matrix.indices, matrix.data.astype(np.float32),
+                                      (M, N), dev)
+        if built is not None:
+            values, rows, cols, morton = built
+            return VOIDTensor(values=values if dtype == torch.float32 else values.to(dtype), block_rows=rows,
+                              block_cols=cols, morton_codes=morton, shape=(M, N), tile_size=(32, 32),
+                              nnz_original=nnz, n_blocks=int(values.shape[0]),
+                              density=values.shape[0] / (n_br * n_bc) if n_br * n_bc else 0.0, dtype=dtype)
+
     coo = matrix.tocoo()
     rows = np.asarray(coo.row, dtype=np.int64)
     cols = np.asarray(coo.col, dtype=np.int64)
