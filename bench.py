@@ -51,9 +51,10 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
-    ap.add_argument("--op", default="spmm", choices=["spmm", "quantize", "format"],
+    ap.add_argument("--op", default="spmm", choices=["spmm", "quantize", "format", "float"],
                     help="spmm (default): the SpMM; quantize: device per-tile INT8 quantisation of the config's "
-                         "A tiles; format: device CSR -> VOID tiles of the config's A")
+                         "A tiles; format: device CSR -> VOID tiles of the config's A; float: the float "
+                         "SpMM (void_spmm) on the config's fp32 tiles and fp32 B")
     ap.add_argument("--epilogue", default=None, help="int8 epilogue (default per_block)")
     ap.add_argument("--chunk", type=int, default=None, help="override the Stream-K chunk")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
@@ -200,6 +201,66 @@ def run_for_counters(prob, steps: int):
     torch.cuda.synchronize()
 
 
+FP32_PEAK_TFLOPS = 157.3  # dense MFMA fp32, MI355X
+
+
+def bench_float(args, dev):
+    """void_spmm on fp32 tiles and fp32 B of a config (the reference's float
+    path), fp32 MFMA; CPU baseline: the torch-CPU tile path in fp32."""
+    import torch
+
+    import cases
+    import oracle
+    import void_amd
+    case = {"c2": cases.c2_int8, "c3": cases.c3_fp8, "c4": cases.c4_powerlaw, "c5": cases.c5_ffn}[args.config]()
+    vt = cases.make_void_tensor(case, "cpu").to(dev)
+    B = torch.from_numpy(case.b).to(dev)
+    out = torch.empty(case.M, case.N, device=dev)
+    run = lambda: void_amd.void_spmm(vt, B, out=out)
+    nb = vt.n_blocks
+    ops = 2.0 * nb * 1024 * case.N
+    nbytes = nb * (4096 + 4) + 4 * (vt.block_grid[0] + 1) + 4 * case.K * case.N + 4 * case.M * case.N
+    cold, hot, wall = time_gpu({"run": run}, args.steps, args.warmup, flush=True)
+    t_mem, t_ops = nbytes / (HBM_PEAK_GBS * 1e9), ops / (FP32_PEAK_TFLOPS * 1e12)
+    tflops = ops / (cold * 1e-3) / 1e12
+    if t_ops >= t_mem:
+        roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tflops / FP32_PEAK_TFLOPS, 4)}
+    else:
+        gbs = nbytes / (cold * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    roof.update(traffic=None, algorithmic_bytes=nbytes)
+    cpu = None
+    if args.cpu_seconds > 0:
+        tiles = torch.from_numpy(case.tiles)
+        rows = torch.from_numpy(case.block_rows.astype(np.int64))
+        cols = torch.from_numpy(case.block_cols.astype(np.int64))
+        ones = torch.ones(nb)
+        bh = torch.from_numpy(case.b)
+        torch.set_num_threads(len(os.sched_getaffinity(0)))
+        times, t_end = [], time.perf_counter() + args.cpu_seconds
+        while True:
+            t = time.perf_counter()
+            oracle.cpu_baseline_spmm(tiles, ones, cols, rows, bh, case.M)
+            times.append(time.perf_counter() - t)
+            if time.perf_counter() > t_end and len(times) >= 3:
+                break
+        med = statistics.median(times[1:]) if len(times) > 1 else times[0]
+        cpu = {"value": round(ops / med / 1e12, 4), "unit": "TFLOP/s", "cores": len(os.sched_getaffinity(0)),
+               "kind": "port", "ms": round(med * 1e3, 3),
+               "sample": f"full {args.config} problem in fp32, torch CPU tile bmm + index_add, median of {len(times) - 1} reps"}
+    line = {"metric": f"FP32 BSpMM effective TFLOP/s (void_spmm), {case.name} in fp32", "value": round(tflops, 3),
+            "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(cold, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f32", "data": "synthetic (seeded generators of BASELINE.json configs)",
+            "config": {"workload": case.name, "op": "float", "M": case.M, "K": case.K, "N": case.N, "n_tiles": nb,
+                       "cache": "cold (1 GiB overwrite between steps)"},
+            "roofline": roof, "cpu_baseline": cpu,
+            "extra": {"hot_ms": round(hot, 5), "wall_s": round(wall, 3)}}
+    print(json.dumps(line), flush=True)
+
+
 def bench_input_side(args, dev):
     """The device quantiser or the device CSR -> tiles conversion on the A
     operand of a config, timed like the SpMM (cold: after a 1 GiB overwrite),
@@ -314,6 +375,9 @@ def main():
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
+    if args.op == "float":
+        bench_float(args, dev)
+        return
     if args.op != "spmm":
         bench_input_side(args, dev)
         return

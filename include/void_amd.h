@@ -166,6 +166,17 @@ int void_spmm_int8(const void_bsr_desc* a, const void_dense_args* d, int32_t epi
 int void_spmm_fp8(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
                   void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Float SpMM: fp32 tiles times fp32 B on the fp32 MFMA (exact products,
+ * fp32 accumulation), then bias, activation and conversion to d->out_dtype
+ * (f32, bf16 or f16).  Replaces void_spmm_kernel + void_spmm
+ * (void/ops.py:148-213) and, with d->activation / d->bias set,
+ * void_spmm_activation_kernel (void/fusion.py:98-198) for float VOID
+ * tensors.  a->tiles holds fp32 tiles; a->scales, d->b_scale and
+ * d->b_scale_vec are not used.  B row-major; plan items of at most 64
+ * tiles (plan->chunk_tiles <= 64); workspace as for void_spmm_int8. */
+int void_spmm_f32(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
+                  void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* ---- Quantisers on the path's input side (one wave per tile) ---------- */
 
 /* Per-tile symmetric INT8 of n_tiles fp32 32x32 tiles (tile t at

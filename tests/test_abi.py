@@ -151,6 +151,10 @@ def test_spmm_fails_loudly_on_cpu_tensors():
     f8 = void_amd.void_tensor_to_fp8(vt)
     with pytest.raises(RuntimeError, match="GPU"):
         void_amd.void_spmm_fp8(f8, torch.randn(64, 16))
+    with pytest.raises(RuntimeError, match="GPU"):
+        void_amd.void_spmm(vt, torch.randn(64, 16))
+    with pytest.raises(RuntimeError, match="GPU"):
+        void_amd.void_spmm_gelu(vt, torch.randn(64, 16))
 
 
 def test_missing_library_raises(monkeypatch, tmp_path):

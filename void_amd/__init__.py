@@ -45,6 +45,7 @@ from .fp8 import (
     void_tensor_to_fp8,
 )
 from .fusion import ActivationType, get_activation_code, void_spmm_gelu, void_spmm_relu, void_spmm_silu
+from .ops import void_spmm
 from .stream_k import StreamKWorkload, analyze_workload_balance, compute_stream_k_workload
 
 __version__ = "0.1.0"

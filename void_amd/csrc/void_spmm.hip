@@ -1147,6 +1147,199 @@ int launch_cg(const Params& p, int grid, hipStream_t stream) {
 // aligned rows), or bytewise (anything else).
 enum Layout { kColVec, kColByte, kRowLds, kRowVec, kRowByte };
 
+// ---------------------------------------------------------------------------
+// Float kernel (void_spmm_f32): fp32 tiles times fp32 B, the reference's
+// float path (void_spmm, ops.py:148-213, and the activation kernel of
+// fusion.py:98-198), on v_mfma_f32_32x32x2_f32: exact fp32 products with
+// fp32 accumulation, no quantisation.
+//
+// One workgroup = 4 waves on one work item x one 128-column panel.  The
+// waves take the item's tiles round-robin (wave w: tiles w, w+4, ...) and
+// each computes all 128 columns as four 32x32 accumulators; lane (j, g)
+// feeds MFMA c with column 4j + c, so one 16-byte load brings it four
+// columns' values of one B row.  A tile: lane (j, g) holds row j, k = 16g ..
+// 16g+15 (four 16-byte loads); MFMA s (s < 16) takes k = 16g + s from both
+// operands, so the k order agrees for A and B.  Per tile and wave: 20 loads
+// and 64 MFMAs of 64 cycles -- the kernel is MFMA-bound, so the next tile's
+// loads (one tile ahead) hide the memory latency.  Partial sums of the four
+// waves meet in LDS, as in spmm_bsr_kernel, and split rows use the same
+// coherent fix-up.
+constexpr int kEltF32 = 2;
+
+struct F32Tile {
+  v4f a[4];   // A[j][16g + 4q .. 16g + 4q + 3]
+  v4f b[16];  // B[32 kb + 16g + s][col0 .. col0 + 3]
+};
+
+template <int OUT, bool VEC>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void spmm_f32_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) float red[kWaves][kTile][kRedStride];
+  int& s_last = *reinterpret_cast<int*>(&red[0][0][kPanel]);  // padding word: split-row arrival flag
+
+  TRACE_DECL;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int j = lane & 31, g = lane >> 5;
+
+  const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  int item_idx, panel;
+  wg_tile(L, p.n_items, p.n_panels, p.panel_group, item_idx, panel);
+  const void_work_item* itp = p.items + item_idx;
+  const int row = itp->row, begin = itp->begin, end = itp->end, split_tile = itp->tile;
+  const int nt = end - begin;
+  const int col0 = panel * kPanel + j * kColsPerLane;
+  TRACE_POINT(0);
+
+  const float* tiles = reinterpret_cast<const float*>(p.tiles);
+  const float* B = reinterpret_cast<const float*>(p.b);
+  // Block column of tile i (i < 64) in lane i; the host keeps items at <= 64 tiles.
+  const int col_64 = nt > 0 ? p.col_idx[begin + min(lane, nt - 1)] : 0;
+  const int bcol = col0 < p.N ? col0 : 0;  // past N: any valid column, never stored
+
+  float sb = 1.f, bias[4];
+  {
+    const float* bip = p.bias ? p.bias : reinterpret_cast<const float*>(p.row_ptr);
+    const int cmax = p.bias ? p.N - 1 : 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) bias[c] = p.bias ? bip[min(col0 + c, cmax)] : 0.f;
+  }
+  (void)sb;
+
+  v16f acc[kColsPerLane] = {};
+  auto load = [&](F32Tile& x, int idx) {  // idx < nt, wave-uniform
+    const int kb = __builtin_amdgcn_readlane(col_64, idx);
+    const float* ap = tiles + (int64_t)(begin + idx) * (kTile * kTile) + j * kTile + 16 * g;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) x.a[q] = *reinterpret_cast<const v4f*>(ap + 4 * q);
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int k = min(kb * kTile + 16 * g + s, p.K - 1);  // rows past K meet A's zero padding
+      const float* bp = B + (int64_t)k * p.ldb;
+      if constexpr (VEC) {
+        x.b[s] = *reinterpret_cast<const v4f*>(bp + bcol);
+      } else {
+        v4f v;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = bp[min(col0 + c, p.N - 1)];
+        x.b[s] = v;
+      }
+    }
+  };
+  auto consume = [&](const F32Tile& x) {
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const float a = x.a[s >> 2][s & 3];
+#pragma unroll
+      for (int c = 0; c < kColsPerLane; ++c)
+        acc[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, x.b[s][c], acc[c], 0, 0, 0);
+    }
+  };
+  if (wave < nt) {
+    // Unrolled by two with fixed buffers; the load of the next tile is
+    // unconditional (past the end it re-reads the current one), which keeps
+    // the compiler's vmcnt waits exact.
+    F32Tile X, Y;
+    load(X, wave);
+    for (int i = wave;;) {
+      load(Y, i + kWaves < nt ? i + kWaves : i);
+      consume(X);
+      i += kWaves;
+      if (i >= nt) break;
+      load(X, i + kWaves < nt ? i + kWaves : i);
+      consume(Y);
+      i += kWaves;
+      if (i >= nt) break;
+    }
+  }
+  TRACE_POINT(2);
+
+  // Cross-wave reduction.  MFMA result layout: lane (j, g), register r holds
+  // row 8 (r / 4) + 4 g + r % 4; MFMA c holds column 4j + c.
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int rr = 8 * (r >> 2) + 4 * g + (r & 3);
+    *reinterpret_cast<v4f*>(&red[wave][rr][red_col(rr, 4 * j)]) = v4f{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+  }
+  __syncthreads();
+  v4f sum[kRowsPerWave / 2];
+#pragma unroll
+  for (int i = 0; i < kRowsPerWave / 2; ++i) {
+    const int rr = wave * kRowsPerWave + 2 * i + g;
+    v4f s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) s += *reinterpret_cast<const v4f*>(&red[w][rr][red_col(rr, 4 * j)]);
+    sum[i] = s;
+  }
+  TRACE_POINT(3);
+
+  if (split_tile >= 0) {
+    // Split row: the same coherent publish / count / reduce-in-chunk-order
+    // protocol as spmm_bsr_kernel.
+    const int nchunks = itp->nchunks, slot = itp->slot, chunk = itp->chunk;
+    const size_t tile_elems = (size_t)kTile * kPanel;
+    int* part = static_cast<int*>(p.partials);
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave / 2; ++i) {
+      const int rr = wave * kRowsPerWave + 2 * i + g;
+      const size_t off = ((size_t)(slot + chunk) * p.n_panels + panel) * tile_elems + (size_t)rr * kPanel + 4 * j;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        __hip_atomic_store(part + off + c, __float_as_int(sum[i][c]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    unsigned* ctr = p.counters + (size_t)split_tile * p.n_panels + panel;
+    if (tid == 0) {
+      const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = (old == (unsigned)(nchunks - 1));
+    }
+    __syncthreads();
+    if (!s_last) {
+      TRACE_FLUSH();
+      return;
+    }
+    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave / 2; ++i) {
+      const int rr = wave * kRowsPerWave + 2 * i + g;
+      v4f s = {0.f, 0.f, 0.f, 0.f};
+      for (int ch = 0; ch < nchunks; ++ch) {
+        const size_t off = ((size_t)(slot + ch) * p.n_panels + panel) * tile_elems + (size_t)rr * kPanel + 4 * j;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          s[c] += __int_as_float(__hip_atomic_load(part + off + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      }
+      sum[i] = s;
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < kRowsPerWave / 2; ++i) {
+    const int rr = wave * kRowsPerWave + 2 * i + g;
+    float v[4];
+    int vi[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float x = sum[i][c];
+      if (p.bias) x = __fadd_rn(x, bias[c]);
+      v[c] = activate(x, p.activation);
+      vi[c] = 0;
+    }
+    store4<OUT, VEC>(p, row * kTile + rr, col0, v, vi);
+  }
+  TRACE_POINT(4);
+  TRACE_FLUSH();
+}
+
+template <int OUT, bool VEC>
+int launch_f32(const Params& p, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL((spmm_f32_kernel<OUT, VEC>), dim3(grid), dim3(kThreads), 0, stream, p);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(VOID_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return VOID_OK;
+}
+
 template <int ELT, int EPI, int OUT>
 int launch_layout(const Params& p, int grid, hipStream_t s, int layout) {
   switch (layout) {
@@ -1190,7 +1383,7 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
   if (!d->c) return fail(VOID_ERR_ARG, "null output pointer");
   if (!items || n_items <= 0) return fail(VOID_ERR_ARG, "empty work list for M=%d", a->M);
   if (!a->row_ptr) return fail(VOID_ERR_ARG, "null row_ptr");
-  if (a->n_blocks > 0 && (!a->tiles || !a->col_idx || !a->scales || !d->b))
+  if (a->n_blocks > 0 && (!a->tiles || !a->col_idx || (!a->scales && elt != kEltF32) || !d->b))
     return fail(VOID_ERR_ARG, "null tile, column, scale or B pointer");
   if (d->ldc < d->N) return fail(VOID_ERR_ARG, "ldc %lld < N %d", (long long)d->ldc, d->N);
   if (d->b_col_major ? d->ldb < a->K : d->ldb < d->N)
@@ -1201,6 +1394,9 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
     return fail(VOID_ERR_UNSUPPORTED, "RAW_I32 epilogue and I32 output go together");
   if (elt == kEltFp8 && epilogue != VOID_EPI_PER_BLOCK)
     return fail(VOID_ERR_UNSUPPORTED, "fp8 SpMM supports only the per-block epilogue");
+  if (elt == kEltF32 && d->b_col_major) return fail(VOID_ERR_UNSUPPORTED, "float SpMM takes a row-major B");
+  if (elt == kEltF32 && plan->chunk_tiles > 64)
+    return fail(VOID_ERR_ARG, "float SpMM takes work items of at most 64 tiles (chunk_tiles %d)", plan->chunk_tiles);
   if (d->activation < VOID_ACT_NONE || d->activation > VOID_ACT_SILU)
     return fail(VOID_ERR_ARG, "unknown activation %d", d->activation);
 
@@ -1249,6 +1445,16 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
   else
     layout = (c_ok && (bu % 4 == 0) && (d->ldb % 4 == 0)) ? kRowVec : kRowByte;
   const int grid = (int)grid64;
+
+  if (elt == kEltF32) {
+    const bool vec = c_ok && (bu % 16 == 0) && (d->ldb % 4 == 0) && (d->N % 4 == 0);
+    switch (d->out_dtype) {
+      case VOID_DT_F32: return vec ? launch_f32<VOID_DT_F32, true>(p, grid, stream) : launch_f32<VOID_DT_F32, false>(p, grid, stream);
+      case VOID_DT_BF16: return vec ? launch_f32<VOID_DT_BF16, true>(p, grid, stream) : launch_f32<VOID_DT_BF16, false>(p, grid, stream);
+      case VOID_DT_F16: return vec ? launch_f32<VOID_DT_F16, true>(p, grid, stream) : launch_f32<VOID_DT_F16, false>(p, grid, stream);
+      default: return fail(VOID_ERR_UNSUPPORTED, "float SpMM writes f32, bf16 or f16");
+    }
+  }
 
   // The column-group kernel addresses every operand with 31-bit buffer
   // offsets; larger operands and the other B layouts use spmm_bsr_kernel.
@@ -1397,6 +1603,12 @@ int void_spmm_int8(const void_bsr_desc* a, const void_dense_args* d, int32_t epi
 int void_spmm_fp8(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
                   void* workspace, size_t workspace_bytes, hipStream_t stream) {
   return run(kEltFp8, a, d, VOID_EPI_PER_BLOCK, plan, workspace, workspace_bytes, stream);
+}
+
+int void_spmm_f32(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
+                  void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (d && d->out_dtype == VOID_DT_I32) return fail(VOID_ERR_UNSUPPORTED, "float SpMM writes f32, bf16 or f16");
+  return run(kEltF32, a, d, VOID_EPI_PER_BLOCK, plan, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

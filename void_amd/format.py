@@ -106,6 +106,20 @@ class VOIDTensor:
     n_blocks: int
     density: float
     dtype: torch.dtype = torch.float32
+    _device_bsr: dict = field(default_factory=dict, repr=False, compare=False)
+
+    def device_bsr(self):
+        """Block-row-major fp32 device copy of the tiles for the float kernel
+        (built once per device)."""
+        from . import _runtime
+        key = str(self.values.device)
+        d = self._device_bsr.get(key)
+        if d is None:
+            ones = torch.ones(1, dtype=torch.float32, device=self.values.device)
+            d = _runtime.make_device_bsr(self.values.to(torch.float32).contiguous(), ones, self.block_rows,
+                                         self.block_cols, self.shape, self.tile_size, self.values.device, True)
+            self._device_bsr[key] = d
+        return d
 
     @property
     def padded_shape(self) -> Tuple[int, int]:

@@ -78,15 +78,32 @@ def _spmm_activation(a, b: torch.Tensor, bias: Optional[torch.Tensor], out: Opti
     if isinstance(a, FP8VOIDTensor):
         return void_spmm_fp8(a, b, output_dtype=out_dtype, b_scale=b_scale, activation=activation,
                              bias=bias, out=out)
-    raise NotImplementedError(
-        "the gfx950 fused SpMM takes quantised tiles (Int8VOIDTensor or FP8VOIDTensor); quantise the "
-        "VOIDTensor with quantize_void_tensor or void_tensor_to_fp8 first")
+    from .format import VOIDTensor
+    if isinstance(a, VOIDTensor):
+        # Float tiles: the reference's own case (fusion.py:444-511), fp32 MFMA
+        # kernel; output in B's dtype.  An all-empty A keeps the reference's
+        # torch activation of the bias (fusion.py:466-476).
+        from .ops import float_spmm
+        if a.n_blocks == 0:
+            res = torch.zeros(a.shape[0], b.shape[1], dtype=b.dtype, device=b.device) if out is None else out.zero_()
+            if bias is not None:
+                res[:, :] = bias[None, :]
+                res = apply_activation_torch(res, activation)
+                if out is not None and res is not out:
+                    out.copy_(res)
+                    res = out
+            return res
+        return float_spmm(a, b, out=out, bias=bias, activation=get_activation_code(activation))
+    raise TypeError(f"unsupported sparse operand {type(a).__name__}")
 
 
 def void_spmm_gelu(a, b: torch.Tensor, bias: Optional[torch.Tensor] = None,
                    out: Optional[torch.Tensor] = None, *, b_scale=None,
                    out_dtype: Optional[torch.dtype] = None, epilogue: Optional[str] = None) -> torch.Tensor:
-    """C = GELU(A @ B + bias) (fusion.py:381-399) with a quantised A.
+    """C = GELU(A @ B + bias) (fusion.py:381-399).
+
+    Float VOIDTensor A: the reference's case, fp32 kernel, output in B's
+    dtype.
 
     Int8VOIDTensor A: float B is quantised per tensor as void_spmm_int8
     does; an int8 B with b_scale (scalar or per column) uses the per-block

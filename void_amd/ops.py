@@ -1,0 +1,76 @@
+"""Float SpMM on VOID tiles (void/ops.py:148-213): C = A @ B with fp32
+tiles, on the fp32 MFMA kernel of libvoid_amd.so (void_spmm_f32)."""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _lib, _runtime
+
+# Longest work item of the float kernel: it holds an item's block columns in
+# one register per lane.
+F32_CHUNK = 64
+
+
+def float_spmm(a, b: torch.Tensor, *, out: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
+               activation: int = _lib.ACT_NONE) -> torch.Tensor:
+    """activation(A @ B + bias) for a float VOIDTensor A; the output has B's
+    dtype (f32, bf16 or f16), as the reference's kernels write."""
+    if b.dim() != 2:
+        raise ValueError("B must be 2-D")
+    M, K = a.shape
+    if K != b.shape[0]:
+        raise ValueError(f"A is {M}x{K} but B has {b.shape[0]} rows")
+    _runtime.require_gpu(b, "B")
+    N = b.shape[1]
+    out_dtype = b.dtype if b.dtype in (torch.float32, torch.bfloat16, torch.float16) else torch.float32
+    if out is None:
+        out = torch.empty(M, N, dtype=out_dtype, device=b.device)
+    elif out.shape != (M, N):
+        raise ValueError(f"out must be [{M}, {N}]")
+    if a.n_blocks == 0:
+        out.zero_()
+        if bias is not None:
+            out[:] = bias[None, :].to(out.dtype)
+        return out
+    _runtime.require_gpu(a.values, "A")
+    if a.values.device != b.device:
+        raise ValueError(f"A on {a.values.device}, B on {b.device}")
+    b32 = b.to(torch.float32).contiguous()
+    if bias is not None:
+        if bias.shape != (N,):
+            raise ValueError(f"bias must be [{N}]")
+        bias = bias.to(device=b.device, dtype=torch.float32).contiguous()
+    dbsr = a.device_bsr()
+    lib = _lib.lib()
+    target = out if (out.stride(1) == 1 and out.stride(0) >= N) else torch.empty_like(out)
+    plan = dbsr.plan(F32_CHUNK)
+    ws, ws_bytes = plan.workspace(N, out.device)
+    cplan = _lib.Plan(items=plan.items.data_ptr(), n_items=plan.n_items, n_split_tiles=plan.n_split_tiles,
+                      n_slots=plan.n_slots, chunk_tiles=plan.chunk)
+    dense = _lib.DenseArgs(b=b32.data_ptr(), ldb=b32.stride(0), b_col_major=0, N=N, b_scale=1.0, b_scale_vec=None,
+                           bias=bias.data_ptr() if bias is not None else None, c=target.data_ptr(),
+                           ldc=target.stride(0), out_dtype=_runtime.out_code(target.dtype), activation=activation)
+    desc = dbsr.desc()
+    st = lib.void_spmm_f32(ctypes.byref(desc), ctypes.byref(dense), ctypes.byref(cplan),
+                           ws.data_ptr() if ws is not None else None, ws_bytes,
+                           torch.cuda.current_stream(out.device).cuda_stream)
+    _lib.check(st, "void_spmm_f32")
+    if target is not out:
+        out.copy_(target)
+    return out
+
+
+def void_spmm(a, b: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """C = A @ B for a float VOIDTensor (ops.py:148-213); C has B's dtype."""
+    from .int_quant import Int8VOIDTensor
+    from .fp8 import FP8VOIDTensor
+    if isinstance(a, (Int8VOIDTensor, FP8VOIDTensor)):
+        raise TypeError("void_spmm takes a float VOIDTensor; use void_spmm_int8 / void_spmm_fp8 for quantised tiles")
+    return float_spmm(a, b, out=out)
+
+
+__all__ = ["void_spmm", "float_spmm"]
