@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define VOID_AMD_ABI_VERSION 1
+#define VOID_AMD_ABI_VERSION 2
 #define VOID_TILE 32
 
 typedef enum void_status {
@@ -120,6 +120,9 @@ typedef struct void_dense_args {
   int64_t ldc;
   int32_t out_dtype;      /* void_dtype */
   int32_t activation;     /* void_activation */
+  int32_t bias_per_row;   /* 0: bias[N] per column; 1: bias[M] per output row (the reference's
+                             row-bias kernel, void/fusion.py:202-304; float SpMM only) */
+  int32_t reserved;       /* 0 */
 } void_dense_args;
 
 /* ---------------------------------------------------------------------- */

@@ -44,7 +44,9 @@ from .fp8 import (
     void_spmm_fp8,
     void_tensor_to_fp8,
 )
-from .fusion import ActivationType, get_activation_code, void_spmm_gelu, void_spmm_relu, void_spmm_silu
+from .fusion import (ActivationType, FusedSparseLinear, get_activation_code, void_spmm_gelu, void_spmm_relu,
+                     void_spmm_silu)
+from .packed import load_packed, pack, save_packed, unpack
 from .ops import void_spmm
 from .stream_k import StreamKWorkload, analyze_workload_balance, compute_stream_k_workload
 

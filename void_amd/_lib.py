@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libvoid_amd.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # enum void_epilogue
 EPI_RAW_I32 = 0
@@ -85,6 +85,8 @@ class DenseArgs(ctypes.Structure):
         ("ldc", c_int64),
         ("out_dtype", c_int32),
         ("activation", c_int32),
+        ("bias_per_row", c_int32),
+        ("reserved", c_int32),
     ]
 
 

@@ -83,6 +83,7 @@ struct Params {
   int32_t activation;
   int32_t n_items;
   int32_t panel_group;  // panels one XCD's share of the grid covers (see wg_tile)
+  int32_t bias_per_row;  // float kernel: bias indexed by output row
 };
 
 #ifdef VOID_TRACE
@@ -1197,14 +1198,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int col_64 = nt > 0 ? p.col_idx[begin + min(lane, nt - 1)] : 0;
   const int bcol = col0 < p.N ? col0 : 0;  // past N: any valid column, never stored
 
-  float sb = 1.f, bias[4];
-  {
-    const float* bip = p.bias ? p.bias : reinterpret_cast<const float*>(p.row_ptr);
-    const int cmax = p.bias ? p.N - 1 : 0;
+  float bias[4] = {0.f, 0.f, 0.f, 0.f};  // per-column bias of this lane's columns
+  if (p.bias && !p.bias_per_row) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) bias[c] = p.bias ? bip[min(col0 + c, cmax)] : 0.f;
+    for (int c = 0; c < 4; ++c) bias[c] = p.bias[min(col0 + c, p.N - 1)];
   }
-  (void)sb;
 
   v16f acc[kColsPerLane] = {};
   auto load = [&](F32Tile& x, int idx) {  // idx < nt, wave-uniform
@@ -1319,14 +1317,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int rr = wave * kRowsPerWave + 2 * i + g;
     float v[4];
     int vi[4];
+    const int grow = row * kTile + rr;
+    const float rbias = (p.bias && p.bias_per_row) ? p.bias[min(grow, p.M - 1)] : 0.f;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       float x = sum[i][c];
-      if (p.bias) x = __fadd_rn(x, bias[c]);
+      if (p.bias) x = __fadd_rn(x, p.bias_per_row ? rbias : bias[c]);
       v[c] = activate(x, p.activation);
       vi[c] = 0;
     }
-    store4<OUT, VEC>(p, row * kTile + rr, col0, v, vi);
+    store4<OUT, VEC>(p, grow, col0, v, vi);
   }
   TRACE_POINT(4);
   TRACE_FLUSH();
@@ -1395,6 +1395,8 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
   if (elt == kEltFp8 && epilogue != VOID_EPI_PER_BLOCK)
     return fail(VOID_ERR_UNSUPPORTED, "fp8 SpMM supports only the per-block epilogue");
   if (elt == kEltF32 && d->b_col_major) return fail(VOID_ERR_UNSUPPORTED, "float SpMM takes a row-major B");
+  if (d->bias_per_row && elt != kEltF32)
+    return fail(VOID_ERR_UNSUPPORTED, "a per-row bias is supported by the float SpMM only");
   if (elt == kEltF32 && plan->chunk_tiles > 64)
     return fail(VOID_ERR_ARG, "float SpMM takes work items of at most 64 tiles (chunk_tiles %d)", plan->chunk_tiles);
   if (d->activation < VOID_ACT_NONE || d->activation > VOID_ACT_SILU)
@@ -1424,6 +1426,7 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
   p.activation = d->activation;
   p.n_items = n_items;
   p.panel_group = n_panels >= 16 ? n_panels / 8 : 1;
+  p.bias_per_row = d->bias_per_row;
   p.items = items;
   p.trace = g_trace;
   if (n_split_tiles > 0) {

@@ -126,5 +126,77 @@ def void_spmm_silu(a, b: torch.Tensor, bias: Optional[torch.Tensor] = None,
     return _spmm_activation(a, b, bias, out, "silu", kw.get("b_scale"), kw.get("out_dtype"), kw.get("epilogue"))
 
 
-__all__ = ["ActivationType", "get_activation_code", "gelu_tanh", "void_spmm_gelu", "void_spmm_relu",
-           "void_spmm_silu"]
+class FusedSparseLinear(torch.nn.Module):
+    """Sparse linear layer y = activation(W x + b) in one kernel
+    (fusion.py:756-836): W is a float VOIDTensor [out_features, in_features],
+    b a per-output-feature (row) bias, the product W @ x^T runs on the fp32
+    MFMA kernel with the bias and activation fused (void_spmm_f32 with
+    bias_per_row), as the reference's row-bias activation kernel does
+    (fusion.py:202-304).  Buffers and fields match the reference so that its
+    state dicts load; ``from_packed`` loads a packed BSR blob straight into
+    the device layout."""
+
+    def __init__(self, in_features: int, out_features: int, void_tensor, activation: str = "gelu",
+                 bias: bool = True):
+        super().__init__()
+        if tuple(void_tensor.shape) != (out_features, in_features):
+            raise ValueError(f"weight is {tuple(void_tensor.shape)}, expected ({out_features}, {in_features})")
+        self.in_features = in_features
+        self.out_features = out_features
+        self.activation = activation
+        self.register_buffer("values", void_tensor.values.clone())
+        self.register_buffer("block_rows", void_tensor.block_rows)
+        self.register_buffer("block_cols", void_tensor.block_cols)
+        self.register_buffer("morton_codes", void_tensor.morton_codes)
+        self.shape = void_tensor.shape
+        self.tile_size = void_tensor.tile_size
+        self.n_blocks = void_tensor.n_blocks
+        if bias:
+            self.bias = torch.nn.Parameter(torch.zeros(out_features))
+        else:
+            self.register_parameter("bias", None)
+        self._vt = None
+        if getattr(void_tensor, "_device_bsr", None):
+            self._vt = self.get_void_tensor()
+            self._vt._device_bsr.update(void_tensor._device_bsr)
+
+    @classmethod
+    def from_packed(cls, blob_or_path, device="cuda", activation: str = "gelu", bias: bool = True):
+        from .packed import load_packed, unpack
+        vt = unpack(blob_or_path, device) if isinstance(blob_or_path, (bytes, bytearray, memoryview)) \
+            else load_packed(blob_or_path, device)
+        out_f, in_f = vt.shape
+        return cls(in_f, out_f, vt, activation=activation, bias=bias).to(device)
+
+    def get_void_tensor(self):
+        """The weight as a VOIDTensor over the module's buffers (fusion.py:793-806)."""
+        from .format import VOIDTensor
+        vt = self._vt
+        if vt is None or vt.values is not self.values:
+            vt = VOIDTensor(values=self.values, block_rows=self.block_rows, block_cols=self.block_cols,
+                            morton_codes=self.morton_codes, shape=tuple(self.shape), tile_size=tuple(self.tile_size),
+                            nnz_original=0, n_blocks=self.n_blocks, density=0.0, dtype=self.values.dtype)
+            self._vt = vt
+        return vt
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        from .ops import float_spmm
+        x_flat = x.reshape(-1, self.in_features)
+        b = x_flat.t().contiguous()  # [in, batch], row-major, as the reference passes it
+        bias = self.bias.detach() if self.bias is not None else None
+        vt = self.get_void_tensor()
+        if vt.n_blocks == 0:
+            y = torch.zeros(self.out_features, b.shape[1], dtype=b.dtype, device=b.device)
+            if bias is not None:
+                y = apply_activation_torch(y + bias[:, None].to(y.dtype), self.activation)
+        else:
+            y = float_spmm(vt, b, bias=bias, activation=get_activation_code(self.activation), bias_per_row=True)
+        return y.t().reshape(x.shape[:-1] + (self.out_features,))
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"activation={self.activation}, bias={self.bias is not None}")
+
+
+__all__ = ["ActivationType", "FusedSparseLinear", "get_activation_code", "gelu_tanh", "void_spmm_gelu",
+           "void_spmm_relu", "void_spmm_silu"]

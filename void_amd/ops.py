@@ -16,9 +16,10 @@ F32_CHUNK = 64
 
 
 def float_spmm(a, b: torch.Tensor, *, out: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
-               activation: int = _lib.ACT_NONE) -> torch.Tensor:
+               activation: int = _lib.ACT_NONE, bias_per_row: bool = False) -> torch.Tensor:
     """activation(A @ B + bias) for a float VOIDTensor A; the output has B's
-    dtype (f32, bf16 or f16), as the reference's kernels write."""
+    dtype (f32, bf16 or f16), as the reference's kernels write.  bias is [N]
+    (per column), or [M] with bias_per_row (fusion.py:202-304)."""
     if b.dim() != 2:
         raise ValueError("B must be 2-D")
     M, K = a.shape
@@ -34,15 +35,15 @@ def float_spmm(a, b: torch.Tensor, *, out: Optional[torch.Tensor] = None, bias: 
     if a.n_blocks == 0:
         out.zero_()
         if bias is not None:
-            out[:] = bias[None, :].to(out.dtype)
+            out[:] = (bias[:, None] if bias_per_row else bias[None, :]).to(out.dtype)
         return out
     _runtime.require_gpu(a.values, "A")
     if a.values.device != b.device:
         raise ValueError(f"A on {a.values.device}, B on {b.device}")
     b32 = b.to(torch.float32).contiguous()
     if bias is not None:
-        if bias.shape != (N,):
-            raise ValueError(f"bias must be [{N}]")
+        if bias.shape != ((M,) if bias_per_row else (N,)):
+            raise ValueError(f"bias must be [{M if bias_per_row else N}]")
         bias = bias.to(device=b.device, dtype=torch.float32).contiguous()
     dbsr = a.device_bsr()
     lib = _lib.lib()
@@ -53,7 +54,8 @@ def float_spmm(a, b: torch.Tensor, *, out: Optional[torch.Tensor] = None, bias: 
                       n_slots=plan.n_slots, chunk_tiles=plan.chunk)
     dense = _lib.DenseArgs(b=b32.data_ptr(), ldb=b32.stride(0), b_col_major=0, N=N, b_scale=1.0, b_scale_vec=None,
                            bias=bias.data_ptr() if bias is not None else None, c=target.data_ptr(),
-                           ldc=target.stride(0), out_dtype=_runtime.out_code(target.dtype), activation=activation)
+                           ldc=target.stride(0), out_dtype=_runtime.out_code(target.dtype), activation=activation,
+                           bias_per_row=int(bias_per_row))
     desc = dbsr.desc()
     st = lib.void_spmm_f32(ctypes.byref(desc), ctypes.byref(dense), ctypes.byref(cplan),
                            ws.data_ptr() if ws is not None else None, ws_bytes,
