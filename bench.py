@@ -51,10 +51,11 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
-    ap.add_argument("--op", default="spmm", choices=["spmm", "quantize", "format", "float"],
+    ap.add_argument("--op", default="spmm", choices=["spmm", "quantize", "format", "float", "sddmm"],
                     help="spmm (default): the SpMM; quantize: device per-tile INT8 quantisation of the config's "
                          "A tiles; format: device CSR -> VOID tiles of the config's A; float: the float "
-                         "SpMM (void_spmm) on the config's fp32 tiles and fp32 B")
+                         "SpMM (void_spmm) on the config's fp32 tiles and fp32 B; sddmm: the backward of A "
+                         "(gradient on the config's nonzero tiles)")
     ap.add_argument("--epilogue", default=None, help="int8 epilogue (default per_block)")
     ap.add_argument("--chunk", type=int, default=None, help="override the Stream-K chunk")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
@@ -215,11 +216,18 @@ def bench_float(args, dev):
     case = {"c2": cases.c2_int8, "c3": cases.c3_fp8, "c4": cases.c4_powerlaw, "c5": cases.c5_ffn}[args.config]()
     vt = cases.make_void_tensor(case, "cpu").to(dev)
     B = torch.from_numpy(case.b).to(dev)
-    out = torch.empty(case.M, case.N, device=dev)
-    run = lambda: void_amd.void_spmm(vt, B, out=out)
     nb = vt.n_blocks
     ops = 2.0 * nb * 1024 * case.N
-    nbytes = nb * (4096 + 4) + 4 * (vt.block_grid[0] + 1) + 4 * case.K * case.N + 4 * case.M * case.N
+    if args.op == "sddmm":
+        from void_amd import _runtime
+        G = torch.randn(case.M, case.N, device=dev)
+        rows, cols = vt.block_rows.to(torch.int32), vt.block_cols.to(torch.int32)
+        run = lambda: _runtime.sddmm_tiles(G, B, rows, cols, (case.M, case.K), torch.float32)
+        nbytes = nb * (4096 + 8) + 4 * case.M * case.N + 4 * case.K * case.N
+    else:
+        out = torch.empty(case.M, case.N, device=dev)
+        run = lambda: void_amd.void_spmm(vt, B, out=out)
+        nbytes = nb * (4096 + 4) + 4 * (vt.block_grid[0] + 1) + 4 * case.K * case.N + 4 * case.M * case.N
     cold, hot, wall = time_gpu({"run": run}, args.steps, args.warmup, flush=True)
     t_mem, t_ops = nbytes / (HBM_PEAK_GBS * 1e9), ops / (FP32_PEAK_TFLOPS * 1e12)
     tflops = ops / (cold * 1e-3) / 1e12
@@ -232,7 +240,28 @@ def bench_float(args, dev):
                 "frac": round(gbs / HBM_PEAK_GBS, 4)}
     roof.update(traffic=None, algorithmic_bytes=nbytes)
     cpu = None
-    if args.cpu_seconds > 0:
+    if args.cpu_seconds > 0 and args.op == "sddmm":
+        Gh, Bh = G.cpu(), case.b
+        rh, ch = case.block_rows.astype(np.int64), case.block_cols.astype(np.int64)
+        Bt = torch.from_numpy(Bh)
+        torch.set_num_threads(len(os.sched_getaffinity(0)))
+
+        def host():  # torch CPU: gather the row and column blocks, batched matmul
+            Gb = Gh.view(-1, 32, case.N)[torch.from_numpy(rh)]
+            Bb = Bt.view(-1, 32, case.N)[torch.from_numpy(ch)]
+            return torch.bmm(Gb, Bb.transpose(1, 2))
+        times, t_end = [], time.perf_counter() + args.cpu_seconds
+        while True:
+            t = time.perf_counter()
+            host()
+            times.append(time.perf_counter() - t)
+            if time.perf_counter() > t_end and len(times) >= 3:
+                break
+        med = statistics.median(times[1:]) if len(times) > 1 else times[0]
+        cpu = {"value": round(ops / med / 1e12, 4), "unit": "TFLOP/s", "cores": len(os.sched_getaffinity(0)),
+               "kind": "port", "ms": round(med * 1e3, 3),
+               "sample": f"full {args.config} tile set, torch CPU gather + bmm, median of {len(times) - 1} reps"}
+    elif args.cpu_seconds > 0:
         tiles = torch.from_numpy(case.tiles)
         rows = torch.from_numpy(case.block_rows.astype(np.int64))
         cols = torch.from_numpy(case.block_cols.astype(np.int64))
@@ -250,11 +279,12 @@ def bench_float(args, dev):
         cpu = {"value": round(ops / med / 1e12, 4), "unit": "TFLOP/s", "cores": len(os.sched_getaffinity(0)),
                "kind": "port", "ms": round(med * 1e3, 3),
                "sample": f"full {args.config} problem in fp32, torch CPU tile bmm + index_add, median of {len(times) - 1} reps"}
-    line = {"metric": f"FP32 BSpMM effective TFLOP/s (void_spmm), {case.name} in fp32", "value": round(tflops, 3),
+    what = "SDDMM backward of A (void_sddmm_f32)" if args.op == "sddmm" else "BSpMM (void_spmm)"
+    line = {"metric": f"FP32 {what} effective TFLOP/s, {case.name} in fp32", "value": round(tflops, 3),
             "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(cold, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": "f32", "data": "synthetic (seeded generators of BASELINE.json configs)",
-            "config": {"workload": case.name, "op": "float", "M": case.M, "K": case.K, "N": case.N, "n_tiles": nb,
+            "config": {"workload": case.name, "op": args.op, "M": case.M, "K": case.K, "N": case.N, "n_tiles": nb,
                        "cache": "cold (1 GiB overwrite between steps)"},
             "roofline": roof, "cpu_baseline": cpu,
             "extra": {"hot_ms": round(hot, 5), "wall_s": round(wall, 3)}}
@@ -375,7 +405,7 @@ def main():
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
-    if args.op == "float":
+    if args.op in ("float", "sddmm"):
         bench_float(args, dev)
         return
     if args.op != "spmm":

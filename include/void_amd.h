@@ -216,6 +216,18 @@ int void_csr_to_tiles(const int32_t* indptr, const int32_t* indices, const float
                       void* workspace, size_t workspace_bytes, int64_t n_blocks, float* values,
                       int32_t* block_rows, int32_t* block_cols, int64_t* morton, hipStream_t stream);
 
+/* ---- Backward: gradient on the nonzero tiles (SDDMM) ------------------ */
+
+/* grad_tiles[t] = grad_c[32 br .. +32, :] @ b[32 bc .. +32, :]^T for every
+ * tile t = (block_rows[t], block_cols[t]) (any order), fp32 products and
+ * accumulation, written as out_dtype (f32, bf16, f16) into [n_blocks, 32, 32].
+ * grad_c is M x N row-major (leading dimension ldg), b is K x N row-major
+ * (ldb); rows past M / K and columns past N count as zero.  Replaces
+ * void_spmm_backward_a_kernel (void/autograd.py:14-97). */
+int void_sddmm_f32(const float* grad_c, int64_t ldg, const float* b, int64_t ldb, const int32_t* block_rows,
+                   const int32_t* block_cols, int32_t n_blocks, int32_t M, int32_t N, int32_t K, void* grad_tiles,
+                   int32_t out_dtype, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

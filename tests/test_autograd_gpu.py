@@ -1,0 +1,79 @@
+"""Backward of the float SpMM: the SDDMM kernel (void_sddmm_f32) against
+float64 products of the same operands, and the autograd wrappers
+(VOIDSpMM, SparseLinear) against float64 dense gradients.  Bound: recursive
+fp32 summation, (n-1) 2^-24 sum|x y| with n the reduction length."""
+
+import numpy as np
+import pytest
+import torch
+
+import cases
+import oracle
+import void_amd
+from void_amd import _runtime
+
+pytestmark = pytest.mark.gpu
+U = 2.0 ** -24
+
+
+@pytest.mark.parametrize("M,K,N,n,seed", [(1024, 2048, 512, 600, 0), (100, 70, 36, 6, 1), (64, 96, 130, 5, 2)])
+def test_sddmm_tiles(gpu, M, K, N, n, seed):
+    rng = np.random.default_rng(seed)
+    nbr, nbc = -(-M // 32), -(-K // 32)
+    flat = rng.choice(nbr * nbc, min(n, nbr * nbc), replace=False)
+    rows, cols = (flat // nbc).astype(np.int32), (flat % nbc).astype(np.int32)
+    G = rng.standard_normal((M, N)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    got = _runtime.sddmm_tiles(torch.from_numpy(G).to(gpu), torch.from_numpy(B).to(gpu),
+                               torch.from_numpy(rows).to(gpu), torch.from_numpy(cols).to(gpu), (M, K), torch.float32)
+    Gp = np.zeros((nbr * 32, N)); Gp[:M] = G
+    Bp = np.zeros((nbc * 32, N)); Bp[:K] = B
+    for t in range(len(rows)):
+        x = Gp[rows[t] * 32:(rows[t] + 1) * 32]
+        y = Bp[cols[t] * 32:(cols[t] + 1) * 32]
+        ref = x @ y.T
+        bound = N * U * (np.abs(x) @ np.abs(y).T)
+        assert np.all(np.abs(got[t].cpu().numpy() - ref) <= bound + 1e-30), t
+
+
+def test_voidspmm_gradients(gpu):
+    case = cases.uniform_blocks(512, 1024, 96, 150, seed=5)
+    vt = cases.make_void_tensor(case, "cpu").to(gpu)
+    mod = void_amd.VOIDSpMM(vt).to(gpu)
+    x = torch.randn(1024, 96, device=gpu, requires_grad=True)
+    w = torch.randn(512, 96, device=gpu)
+    y = mod(x)
+    (y * w).sum().backward()
+    A = oracle.densify(case.tiles, case.block_rows, case.block_cols, (512, 1024)).astype(np.float64)
+    X, W = x.detach().cpu().double().numpy(), w.cpu().double().numpy()
+    assert np.all(np.abs(y.detach().cpu().numpy() - A @ X) <= 32 * 10 * U * (np.abs(A) @ np.abs(X)) + 1e-30)
+    gX = A.T @ W  # dL/dB = A^T dL/dC
+    n_col = np.bincount(case.block_cols, minlength=32).max()
+    assert np.all(np.abs(x.grad.cpu().numpy() - gX) <= 32 * n_col * U * (np.abs(A).T @ np.abs(W)) + 1e-30)
+    gA = W @ X.T  # dense dL/dA; only the tiles' entries are returned
+    tiles = mod.values.grad.cpu().numpy()
+    vals_rows, vals_cols = vt.block_rows.cpu().numpy(), vt.block_cols.cpu().numpy()
+    bound_full = 96 * U * (np.abs(W) @ np.abs(X).T)
+    for t in range(len(tiles)):
+        r, c = vals_rows[t] * 32, vals_cols[t] * 32
+        assert np.all(np.abs(tiles[t] - gA[r:r + 32, c:c + 32]) <= bound_full[r:r + 32, c:c + 32] + 1e-30)
+
+
+def test_sparse_linear_training_step(gpu):
+    case = cases.uniform_blocks(128, 256, 8, 12, seed=9)
+    vt = cases.make_void_tensor(case, "cpu").to(gpu)
+    layer = void_amd.SparseLinear(256, 128, vt).to(gpu)
+    x = torch.randn(4, 5, 256, device=gpu)
+    y = layer(x)
+    assert y.shape == (4, 5, 128)
+    loss = (y ** 2).mean()
+    loss.backward()
+    assert layer.sparse_weight.values.grad.shape == vt.values.shape and layer.bias.grad.shape == (128,)
+    # an optimiser step changes the values in place; the next forward must see them
+    with torch.no_grad():
+        layer.sparse_weight.values.mul_(2.0)
+        layer.bias.zero_()
+    y2 = layer(x)
+    W = oracle.densify(vt.values.cpu().numpy() * 2.0, case.block_rows, case.block_cols, (128, 256))
+    ref = x.reshape(-1, 256).cpu().double().numpy() @ W.T.astype(np.float64)
+    assert np.allclose(y2.detach().reshape(-1, 128).cpu().numpy(), ref, rtol=1e-5, atol=1e-4)

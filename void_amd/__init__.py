@@ -48,6 +48,7 @@ from .fusion import (ActivationType, FusedSparseLinear, get_activation_code, voi
                      void_spmm_silu)
 from .packed import load_packed, pack, save_packed, unpack
 from .ops import void_spmm
+from .autograd import SparseLinear, VOIDSpMM, VOIDSpMMFunction
 from .stream_k import StreamKWorkload, analyze_workload_balance, compute_stream_k_workload
 
 __version__ = "0.1.0"

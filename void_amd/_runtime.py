@@ -118,13 +118,15 @@ class DeviceBsr:
 
 def make_device_bsr(values: torch.Tensor, scales: torch.Tensor, block_rows: torch.Tensor,
                     block_cols: torch.Tensor, shape: Tuple[int, int], tile_size: Tuple[int, int],
-                    device: torch.device, per_tensor: bool) -> DeviceBsr:
+                    device: torch.device, per_tensor: bool, layout=None) -> DeviceBsr:
+    """Gather the tiles into block-row-major order.  ``layout`` (a BsrLayout
+    of the same block structure) skips the host-side ordering."""
     if tuple(tile_size) != (32, 32):
         raise NotImplementedError(f"the gfx950 kernels take 32x32 tiles, got {tile_size}")
     M, K = shape
     n_br = (M + 31) // 32
     n_bc = (K + 31) // 32
-    lay = build_bsr_layout(block_rows, block_cols, n_br, n_bc, device)
+    lay = layout if layout is not None else build_bsr_layout(block_rows, block_cols, n_br, n_bc, device)
     v = values.to(device)
     if v.dtype != torch.uint8:
         v = v.view(torch.uint8)
@@ -258,3 +260,25 @@ def csr_to_tiles(indptr: np.ndarray, indices: np.ndarray, data: np.ndarray, shap
                                          ws.data_ptr(), ws_bytes, n, values.data_ptr(), rows.data_ptr(),
                                          cols.data_ptr(), morton.data_ptr(), stream), "void_csr_to_tiles")
     return values, rows, cols, morton
+
+
+def sddmm_tiles(grad_c: torch.Tensor, b: torch.Tensor, block_rows: torch.Tensor, block_cols: torch.Tensor,
+                shape: Tuple[int, int], out_dtype: torch.dtype) -> torch.Tensor:
+    """[n, 32, 32] gradient of the nonzero tiles: grad_c[rows of t] @ b[cols of t]^T (void_sddmm_f32)."""
+    M, K = shape
+    n = int(block_rows.numel())
+    N = grad_c.shape[1]
+    out = torch.empty((n, 32, 32), dtype=out_dtype, device=grad_c.device)
+    if n == 0:
+        return out
+    if N == 0:
+        return out.zero_()
+    g = grad_c.to(torch.float32).contiguous()
+    bb = b.to(torch.float32).contiguous()
+    rows = block_rows.to(device=g.device, dtype=torch.int32).contiguous()
+    cols = block_cols.to(device=g.device, dtype=torch.int32).contiguous()
+    st = _lib.lib().void_sddmm_f32(g.data_ptr(), g.stride(0), bb.data_ptr(), bb.stride(0), rows.data_ptr(),
+                                   cols.data_ptr(), n, M, N, K, out.data_ptr(), out_code(out_dtype),
+                                   torch.cuda.current_stream(g.device).cuda_stream)
+    _lib.check(st, "void_sddmm_f32")
+    return out

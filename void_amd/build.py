@@ -20,7 +20,7 @@ INCLUDE_DIR = REPO_DIR / "include"
 LIB_PATH = PKG_DIR / "libvoid_amd.so"
 ARCH = "gfx950"
 
-SOURCES = [SRC_DIR / "void_spmm.hip", SRC_DIR / "void_quant.hip", SRC_DIR / "void_format.hip"]
+SOURCES = [SRC_DIR / "void_spmm.hip", SRC_DIR / "void_quant.hip", SRC_DIR / "void_format.hip", SRC_DIR / "void_sddmm.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
