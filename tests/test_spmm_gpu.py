@@ -28,14 +28,13 @@ pytestmark = pytest.mark.gpu
 FP8_TOL = 2.0 ** -13
 
 
-@pytest.fixture(params=["cg", "bsr"])
+@pytest.fixture(params=["cg", "bsr", "rg"])
 def kernel(request, monkeypatch):
-    """Runs a test on the column-group kernel (the default dispatch) and on
-    the general kernel (forced through VOID_AMD_KERNEL=bsr)."""
-    if request.param == "bsr":
-        monkeypatch.setenv("VOID_AMD_KERNEL", "bsr")
-    else:
-        monkeypatch.delenv("VOID_AMD_KERNEL", raising=False)
+    """Runs a test on each SpMM kernel: the column-group kernel (forced with
+    VOID_AMD_KERNEL=cg; the default dispatch takes it for these shapes), the
+    general kernel (=bsr) and the row-grouped kernel (=rg, where its
+    conditions hold; elsewhere the default dispatch runs)."""
+    monkeypatch.setenv("VOID_AMD_KERNEL", request.param)
     return request.param
 
 

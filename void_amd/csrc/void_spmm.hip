@@ -55,6 +55,7 @@ constexpr int kInline = VOID_ITEM_INLINE_COLS;
 constexpr int kRowsPerWave = kTile / kWaves;  // epilogue rows per wave
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -1149,6 +1150,278 @@ int launch_cg(const Params& p, int grid, hipStream_t stream) {
 enum Layout { kColVec, kColByte, kRowLds, kRowVec, kRowByte };
 
 // ---------------------------------------------------------------------------
+// Row-grouped kernel: for dense-ish A (many tiles per block-row), where the
+// B slabs dominate the gathers of the column-group kernel.
+//
+// One workgroup = 8 wave64s = 8 consecutive block-rows (wave w owns row
+// 8·group + w and all 128 columns of the panel, four 32x32 accumulators
+// with columns 32c + j) x one 128-column panel.  The workgroup first builds
+// the union of its rows' block columns in LDS (a bitmap, then a compacted
+// ascending list).  It then walks that list in steps: the B slab of each step
+// is loaded once for the whole workgroup (each wave 4 of its 32 rows, one
+// 8-byte load per lane) and staged in a double-buffered LDS area with the
+// same XOR swizzle as stage_lds; every wave whose row has a tile in that
+// block column loads its A tile and multiplies it against the slab, read
+// back k-contiguous with ds_read_b64_tr_b8.  With 25 % block density a slab
+// serves about 2.2 of the 8 rows, so the B bytes gathered into the CUs drop
+// by that factor against one slab per (tile, panel).  Rows have at most 64
+// tiles (block columns and scales sit one per lane) and are never split.
+constexpr int kRgWaves = 8;
+constexpr int kRgThreads = 64 * kRgWaves;
+constexpr int kRgSteps = 4;        // union steps per batch
+constexpr int kRgMaxKb = 8192;     // block columns the LDS bitmap covers (K <= 262144)
+
+struct RgBatch {
+  v4i a[kRgSteps];       // this wave's A tile of each step (zeros where its row has none)
+  uint2 b[kRgSteps];     // slab row 4 wave + lane / 16, bytes 8 (lane % 16) .. +7
+  int present;           // bit u: this wave's row has a tile at step u
+  int last;              // bit u: step u's slab crosses K
+  int tpos[kRgSteps];    // tile position in the row for present steps
+};
+
+template <int ELT, int EPI, int OUT>
+__global__ __launch_bounds__(kRgThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void spmm_rg_kernel(Params p) {
+  using A = Accum<ELT, EPI>;
+  using Reg = typename A::Reg;
+  constexpr bool kInt = A::kInt;
+  constexpr bool kScales = (EPI == VOID_EPI_PER_BLOCK);
+
+  __shared__ uint32_t bitmap[kRgMaxKb / 32];
+  __shared__ __attribute__((aligned(16))) uint16_t ulist[kRgMaxKb + 2 * kRgSteps];
+  __shared__ int wsum[kRgWaves + 1];
+  __shared__ __attribute__((aligned(16))) uint8_t b_lds[2][kRgSteps][kSlotBytes];
+
+  TRACE_DECL;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int j = lane & 31, g = lane >> 5;
+
+  const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  int grp, panel;
+  wg_tile(L, p.n_items, p.n_panels, p.panel_group, grp, panel);
+  const int n_br = (p.M + kTile - 1) / kTile;
+  const int row = grp * kRgWaves + wave;
+  const bool row_ok = row < n_br;
+  const int rb = row_ok ? p.row_ptr[row] : 0;
+  const int re = row_ok ? p.row_ptr[row + 1] : 0;
+  const int nt = re - rb;  // <= 64 (host check)
+  TRACE_POINT(0);
+
+  // Block column and scale of tile i of the row in lane i (branch-free:
+  // an empty row reads row_ptr[0]).
+  const int* colp = nt > 0 ? p.col_idx : p.row_ptr;
+  const int colv = colp[nt > 0 ? rb + min(lane, nt - 1) : 0];
+  float scv = 0.f;
+  if constexpr (kScales) {
+    const float* sp = nt > 0 ? p.a_scale : reinterpret_cast<const float*>(p.row_ptr);
+    scv = sp[nt > 0 && !p.per_tensor_a ? rb + min(lane, nt - 1) : 0];
+  }
+  // Epilogue inputs: B scales and bias of columns 32c + j.
+  float sb[4], bias[4];
+  {
+    const float* sbp = p.b_scale_vec ? p.b_scale_vec : reinterpret_cast<const float*>(p.row_ptr);
+    const float* bip = p.bias ? p.bias : reinterpret_cast<const float*>(p.row_ptr);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int cc = min(panel * kPanel + 32 * c + j, p.N - 1);
+      const float vs = sbp[p.b_scale_vec ? cc : 0];
+      const float vb = bip[p.bias ? cc : 0];
+      sb[c] = p.b_scale_vec ? vs : p.b_scale;
+      bias[c] = p.bias ? vb : 0.f;
+    }
+  }
+
+  // Union of the group's block columns, ascending, in ulist[0 .. U).
+  const int n_kb = (p.K + kTile - 1) / kTile;
+  const int n_words = (n_kb + 31) / 32;
+  for (int w = tid; w < n_words; w += kRgThreads) bitmap[w] = 0u;
+  __syncthreads();
+  if (lane < nt) atomicOr(&bitmap[colv >> 5], 1u << (colv & 31));
+  __syncthreads();
+  int U;
+  {
+    // n_words <= 256: one word per thread of the first four waves, then a
+    // workgroup-wide exclusive scan of the set-bit counts.
+    const uint32_t bits = tid < n_words ? bitmap[tid] : 0u;
+    const int cnt = __builtin_popcount(bits);
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int base = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kRgWaves; ++w) {
+      const int v = wsum[w];
+      if (w < wave) base += v;
+      total += v;
+    }
+    int pos = base + incl - cnt;
+    uint32_t b = bits;
+    while (b) {
+      const int bit = __builtin_ctz(b);
+      ulist[pos++] = (uint16_t)(tid * 32 + bit);
+      b &= b - 1;
+    }
+    U = total;
+    if (tid < 2 * kRgSteps) ulist[total + tid] = 0;  // steps past the end: block column 0, zero-range loads
+  }
+  __syncthreads();
+
+  const Rsrc ra = make_rsrc(p.tiles), rbm = make_rsrc(p.b);
+  const int voff_a = j * kTile + 16 * g;
+  const int brow = 4 * wave + (lane >> 4);  // this lane's slab row
+  int cb = panel * kPanel + 8 * (lane & 15);
+  cb = cb < p.N ? cb : 0;                   // past N: any valid 8 bytes, never stored
+  const int voff_b = (int)(brow * p.ldb) + cb;
+  int kb_last = -1, voff_b_last = voff_b;
+  if (p.K % kTile) {
+    kb_last = p.K / kTile;
+    voff_b_last = (int)(min(brow, p.K - kb_last * kTile - 1) * p.ldb) + cb;
+  }
+  const int b_kstride = kTile * (int)p.ldb;
+  const int lds_off = brow * kPanel + ((((lane & 15) >> 1) ^ (brow & 7)) << 4) + 8 * (lane & 1);
+
+  Reg acc[kColsPerLane] = {};
+  int cursor = 0;  // next tile of this wave's row
+  auto issue = [&](RgBatch& x, int base) {
+    const v2i w = *reinterpret_cast<const v2i*>(&ulist[base]);
+    int present = 0, last = 0;
+#pragma unroll
+    for (int u = 0; u < kRgSteps; ++u) {
+      const int kb = __builtin_amdgcn_readfirstlane((w[u >> 1] >> (16 * (u & 1))) & 0xffff);
+      const bool live = base + u < U;
+      const int mine = __builtin_amdgcn_readlane(colv, min(cursor, 63));
+      const bool has = live && cursor < nt && mine == kb;
+      x.tpos[u] = cursor;
+      present |= (int)has << u;
+      cursor += has ? 1 : 0;
+      x.a[u] = __builtin_amdgcn_raw_buffer_load_b128(ra, has ? voff_a : kOutOfRange,
+                                                     (rb + (has ? x.tpos[u] : 0)) * (kTile * kTile), 0);
+      const bool lst = kb == kb_last;
+      last |= (int)lst << u;
+      const v2i bv = __builtin_amdgcn_raw_buffer_load_b64(rbm, live ? (lst ? voff_b_last : voff_b) : kOutOfRange,
+                                                           kb * b_kstride, 0);
+      x.b[u] = uint2{(uint32_t)bv[0], (uint32_t)bv[1]};
+    }
+    x.present = present;
+    x.last = last;
+  };
+  auto consume = [&](const RgBatch& x, int bb) {
+    const int buf = bb & 1;
+#pragma unroll
+    for (int u = 0; u < kRgSteps; ++u) {
+      uint2 v = x.b[u];
+      if constexpr (ELT == kEltFp8) {
+        if (((x.last >> u) & 1) && brow >= p.K - kb_last * kTile) v = uint2{0u, 0u};
+      }
+      *reinterpret_cast<uint2*>(&b_lds[buf][u][lds_off]) = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kRgSteps; ++u) {
+      if ((x.present >> u) & 1) {
+        Frag f;
+        f.a = x.a[u];
+#pragma unroll
+        for (int c = 0; c < kColsPerLane; ++c) f.b[c] = read_tr(&b_lds[buf][u][0], c, j, g);
+        A::step(acc, f, kScales ? bcast(scv, x.tpos[u]) : 0.f);
+      }
+    }
+  };
+  if (U > 0) {
+    RgBatch X, Y;
+    issue(X, 0);
+    TRACE_POINT(1);
+    int bb = 0;
+    while (true) {
+      if ((bb + 1) * kRgSteps < U) {
+        issue(Y, (bb + 1) * kRgSteps);
+        consume(X, bb);
+        ++bb;
+        if ((bb + 1) * kRgSteps < U) {
+          issue(X, (bb + 1) * kRgSteps);
+          consume(Y, bb);
+          ++bb;
+          continue;
+        }
+        consume(Y, bb);
+        break;
+      }
+      consume(X, bb);
+      break;
+    }
+  }
+  TRACE_POINT(2);
+  TRACE_POINT(3);
+  if (!row_ok) {
+    TRACE_FLUSH();
+    return;
+  }
+
+  float mul[4] = {1.f, 1.f, 1.f, 1.f};
+  if constexpr (EPI == VOID_EPI_ROW_MEAN) {
+    // int_quant.py:519-526: S = sum fl(s_a * s_b) in tile order, then S / n.
+    const float rs = (nt > 0) ? (p.per_tensor_a ? p.a_scale[0]
+                                                : p.a_scale[rb + min(lane, nt - 1)])
+                              : 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float S = 0.f;
+      for (int q = 0; q < nt; ++q) S = __fadd_rn(S, __fmul_rn(bcast(rs, q), sb[c]));
+      mul[c] = nt > 0 ? __fdiv_rn(S, (float)nt) : 0.f;
+    }
+  } else if constexpr (EPI == VOID_EPI_PER_BLOCK) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) mul[c] = sb[c];
+  }
+  constexpr int esz = (OUT == VOID_DT_F32 || OUT == VOID_DT_I32) ? 4 : 2;
+  const Rsrc rc = make_rsrc(p.c);
+  const int ldc = (int)p.ldc;
+  const int row0 = row * kTile;
+  const int voff_c = ((4 * g) * ldc + panel * kPanel + j) * esz;
+  const bool full = row0 + kTile <= p.M && panel * kPanel + kPanel <= p.N;
+#pragma unroll
+  for (int c = 0; c < kColsPerLane; ++c) {
+    const int col = panel * kPanel + 32 * c + j;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int rr = 8 * (r >> 2) + (r & 3);
+      const int soff = ((row0 + rr) * ldc + 32 * c) * esz;
+      float x;
+      if constexpr (EPI == VOID_EPI_RAW_I32) x = 0.f;
+      else x = __fmul_rn((float)acc[c][r], mul[c]);
+      if (p.bias) x = __fadd_rn(x, bias[c]);
+      x = activate(x, p.activation);
+      if (full || (row0 + rr + 4 * g < p.M && col < p.N)) {
+        if constexpr (OUT == VOID_DT_F32) {
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(x), rc, voff_c, soff, 0);
+        } else if constexpr (OUT == VOID_DT_I32) {
+          __builtin_amdgcn_raw_buffer_store_b32((int)acc[c][r], rc, voff_c, soff, 0);
+        } else {
+          const uint32_t h = OUT == VOID_DT_BF16 ? f32_to_bf16_bits(x) : f32_to_f16_bits(x);
+          __builtin_amdgcn_raw_buffer_store_b16((unsigned short)h, rc, voff_c, soff, 0);
+        }
+      }
+    }
+  }
+  TRACE_POINT(4);
+  TRACE_FLUSH();
+}
+
+template <int ELT, int EPI, int OUT>
+int launch_rg(const Params& p, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL((spmm_rg_kernel<ELT, EPI, OUT>), dim3(grid), dim3(kRgThreads), 0, stream, p);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(VOID_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return VOID_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Float kernel (void_spmm_f32): fp32 tiles times fp32 B, the reference's
 // float path (void_spmm, ops.py:148-213, and the activation kernel of
 // fusion.py:98-198), on v_mfma_f32_32x32x2_f32: exact fp32 products with
@@ -1459,18 +1732,58 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
     }
   }
 
-  // The column-group kernel addresses every operand with 31-bit buffer
-  // offsets; larger operands and the other B layouts use spmm_bsr_kernel.
-  // VOID_AMD_KERNEL=bsr forces the latter (for comparisons).
+  // The column-group and row-grouped kernels address every operand with
+  // 31-bit buffer offsets; larger operands and the other B layouts use
+  // spmm_bsr_kernel.  VOID_AMD_KERNEL=bsr / cg / rg forces a kernel where
+  // it applies (for comparisons and tests).
   const int esz = (d->out_dtype == VOID_DT_BF16 || d->out_dtype == VOID_DT_F16) ? 2 : 4;
   const int64_t kLim = (int64_t)1 << 31;
   const int64_t b_span = d->b_col_major ? (int64_t)d->N * d->ldb
                                         : (int64_t)((a->K + kTile - 1) / kTile) * kTile * d->ldb;
   const char* force = getenv("VOID_AMD_KERNEL");
-  const bool cg_ok = (layout == kRowLds || layout == kColVec) && plan->chunk_tiles <= kCgMaxTiles &&
-                     (int64_t)a->n_blocks * kTile * kTile < kLim &&
-                     b_span < kLim && (int64_t)a->M * d->ldc * esz < kLim &&
-                     !(force && strcmp(force, "bsr") == 0);
+  const bool force_bsr = force && strcmp(force, "bsr") == 0;
+  const bool force_cg = force && strcmp(force, "cg") == 0;
+  const bool force_rg = force && strcmp(force, "rg") == 0;
+  const bool offsets_ok = (int64_t)a->n_blocks * kTile * kTile < kLim && b_span < kLim &&
+                          (int64_t)a->M * d->ldc * esz < kLim;
+
+  // Row-grouped kernel: unsplit rows of at most 64 tiles, row-major B through
+  // LDS.  It gathers fewer B bytes on long rows, but one 8-wave workgroup per
+  // CU with one batch of lookahead keeps too few bytes in flight: on the FFN
+  // config (25 % block density) it measured 240 us against 165 us for the
+  // column-group kernel.  It therefore runs only on request.
+  const int n_groups = (a->n_block_rows + kRgWaves - 1) / kRgWaves;
+  const bool rg_ok = layout == kRowLds && offsets_ok && plan->n_split_tiles == 0 && plan->chunk_tiles <= 64 &&
+                     (a->K + kTile - 1) / kTile <= kRgMaxKb;
+  if (rg_ok && force_rg) {
+    Params q = p;
+    q.n_items = n_groups;
+    const int rgrid = n_groups * n_panels;
+    auto go = [&](auto elt_c, auto epi_c) -> int {
+      constexpr int E = decltype(elt_c)::value, P = decltype(epi_c)::value;
+      if constexpr (P == VOID_EPI_RAW_I32) {
+        return launch_rg<E, P, VOID_DT_I32>(q, rgrid, stream);
+      } else {
+        switch (d->out_dtype) {
+          case VOID_DT_F32: return launch_rg<E, P, VOID_DT_F32>(q, rgrid, stream);
+          case VOID_DT_BF16: return launch_rg<E, P, VOID_DT_BF16>(q, rgrid, stream);
+          case VOID_DT_F16: return launch_rg<E, P, VOID_DT_F16>(q, rgrid, stream);
+          default: return fail(VOID_ERR_UNSUPPORTED, "out_dtype %d not supported with this epilogue", d->out_dtype);
+        }
+      }
+    };
+    using I8 = std::integral_constant<int, kEltI8>;
+    using F8 = std::integral_constant<int, kEltFp8>;
+    if (elt == kEltFp8) return go(F8{}, std::integral_constant<int, VOID_EPI_PER_BLOCK>{});
+    switch (epilogue) {
+      case VOID_EPI_RAW_I32: return go(I8{}, std::integral_constant<int, VOID_EPI_RAW_I32>{});
+      case VOID_EPI_ROW_MEAN: return go(I8{}, std::integral_constant<int, VOID_EPI_ROW_MEAN>{});
+      default: return go(I8{}, std::integral_constant<int, VOID_EPI_PER_BLOCK>{});
+    }
+  }
+
+  const bool cg_ok = (layout == kRowLds || layout == kColVec) && plan->chunk_tiles <= kCgMaxTiles && offsets_ok &&
+                     !force_bsr;
   if (cg_ok) {
     const bool bcol = layout == kColVec;
     auto go = [&](auto elt_c, auto epi_c) -> int {
