@@ -201,7 +201,7 @@ int void_quantize_tiles_fp8(const float* tiles, int32_t n_tiles, uint8_t* q, flo
 
 /* ---- CSR -> VOID tiles on the device (csr_to_void, void/format.py:248-349) --
  * Canonical CSR (int32 indptr[M+1] and column indices, no duplicate
- * entries; float32 values) becomes Morton-ordered 32x32 fp32 tiles, block
+ * entries; float32 values; indices and values 16-byte aligned) becomes Morton-ordered 32x32 fp32 tiles, block
  * rows, block columns and Morton codes, the reference's VOIDTensor fields.
  * Explicit zeros activate their tile, as in the reference.  Two calls:
  * void_csr_count_blocks writes the number of active blocks to *n_blocks (a

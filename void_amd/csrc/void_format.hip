@@ -108,6 +108,26 @@ __global__ __launch_bounds__(kThreads) void fill_f32(float* p, int64_t n) {
     p[i] = 0.f;
 }
 
+// Entries [b, e) of one CSR row, four per lane per step: the 16-byte-aligned
+// middle with vector loads, the unaligned head and the tail one by one.
+template <typename F>
+__device__ __forceinline__ void for_row_entries(int32_t b, int32_t e, int lane, const int32_t* __restrict__ indices,
+                                                const float* __restrict__ data, F&& f) {
+  const int32_t head_end = min(e, (b + 3) & ~3);
+  for (int32_t j = b + lane; j < head_end; j += 64) f(indices[j], data ? data[j] : 0.f);
+  const int32_t body_end = head_end + ((e - head_end) & ~3);
+  for (int32_t j = head_end + 4 * lane; j < body_end; j += 256) {
+    const int4 c = *reinterpret_cast<const int4*>(indices + j);
+    float4 v = {0.f, 0.f, 0.f, 0.f};
+    if (data) v = *reinterpret_cast<const float4*>(data + j);
+    f(c.x, v.x);
+    f(c.y, v.y);
+    f(c.z, v.z);
+    f(c.w, v.w);
+  }
+  for (int32_t j = body_end + lane; j < e; j += 64) f(indices[j], data ? data[j] : 0.f);
+}
+
 // 1. One wave per CSR row: flag the blocks of its entries.
 __global__ __launch_bounds__(kThreads) void mark_blocks(const int32_t* __restrict__ indptr,
                                                         const int32_t* __restrict__ indices, int32_t M,
@@ -116,7 +136,8 @@ __global__ __launch_bounds__(kThreads) void mark_blocks(const int32_t* __restric
   if (r >= M) return;
   const int lane = threadIdx.x & 63;
   uint8_t* row_flags = flags + (int64_t)(r / kT) * n_bc;
-  for (int32_t j = indptr[r] + lane; j < indptr[r + 1]; j += 64) row_flags[indices[j] / kT] = 1;
+  for_row_entries(indptr[r], indptr[r + 1], lane, indices, nullptr,
+                  [&](int32_t c, float) { row_flags[c / kT] = 1; });
 }
 
 __device__ __forceinline__ bool flag_at(const uint8_t* flags, const Geometry& g, int64_t code, int32_t& br,
@@ -222,10 +243,9 @@ __global__ __launch_bounds__(kThreads) void scatter_entries(const int32_t* __res
   const int lane = threadIdx.x & 63;
   const int32_t* row_rank = rank + (int64_t)(r / kT) * n_bc;
   const int rr = r % kT;
-  for (int32_t j = indptr[r] + lane; j < indptr[r + 1]; j += 64) {
-    const int32_t c = indices[j];
-    values[(int64_t)row_rank[c / kT] * (kT * kT) + rr * kT + (c % kT)] = data[j];
-  }
+  for_row_entries(indptr[r], indptr[r + 1], lane, indices, data, [&](int32_t c, float v) {
+    values[(int64_t)row_rank[c / kT] * (kT * kT) + rr * kT + (c % kT)] = v;
+  });
 }
 
 int launched() {
@@ -258,6 +278,7 @@ int void_csr_count_blocks(const int32_t* indptr, const int32_t* indices, int32_t
     return void_internal_fail(VOID_ERR_UNSUPPORTED, "block grid too large for the device conversion");
   if (!indptr || !workspace || !n_blocks || (M > 0 && !indices))
     return void_internal_fail(VOID_ERR_ARG, "null indptr, indices, workspace or count pointer");
+  if ((uintptr_t)indices % 16) return void_internal_fail(VOID_ERR_ARG, "indices must be 16-byte aligned");
   if (workspace_bytes < ws_bytes(g)) return void_internal_fail(VOID_ERR_WORKSPACE, "workspace too small");
   const Ws w = carve(workspace, g);
   const int64_t nb = (int64_t)g.n_br * g.n_bc;
@@ -286,6 +307,8 @@ int void_csr_to_tiles(const int32_t* indptr, const int32_t* indices, const float
   if (n_blocks == 0) return VOID_OK;
   if (!indptr || !indices || !data || !workspace || !values || !block_rows || !block_cols || !morton)
     return void_internal_fail(VOID_ERR_ARG, "null pointer");
+  if ((uintptr_t)indices % 16 || (uintptr_t)data % 16)
+    return void_internal_fail(VOID_ERR_ARG, "indices and data must be 16-byte aligned");
   if (workspace_bytes < ws_bytes(g)) return void_internal_fail(VOID_ERR_WORKSPACE, "workspace too small");
   const Ws w = carve(workspace, g);
   hipLaunchKernelGGL(rank_blocks, dim3((unsigned)g.n_chunks), dim3(kThreads), 0, stream, g, w.flags, w.chunk,

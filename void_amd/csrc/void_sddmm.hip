@@ -5,12 +5,14 @@
 //   grad[t] = dC[32 br_t .. +32, :] @ B[32 bc_t .. +32, :]^T     (32 x 32)
 //
 // for every active tile t — a sampled dense-dense product on the tiles'
-// support.  One wave64 per tile computes its 32x32 result on
-// v_mfma_f32_32x32x2_f32 (exact fp32 products, fp32 accumulation), reducing
-// over N in chunks of 32: lane (i, g) loads 16 consecutive values of row i of
-// each operand (n = n0 + 16g .. +15) and MFMA s (s < 16) takes n = n0 + 16g + s
-// from both, so the reduction order agrees for the two operands.  The loads
-// of the next chunk are in flight during the 16 MFMAs of the current one.
+// support.  One workgroup of 4 wave64s per tile: wave w reduces the chunks
+// w, w+4, ... of 32 columns of N on v_mfma_f32_32x32x2_f32 (exact fp32
+// products, fp32 accumulation), and the four partial 32x32 blocks are summed
+// through LDS in wave order.  Within a chunk lane (i, g) loads 16 consecutive
+// values of row i of each operand (n = n0 + 16g .. +15) and MFMA s (s < 16)
+// takes n = n0 + 16g + s from both, so the reduction order agrees for the two
+// operands.  The loads of a wave's next chunk are in flight during the 16
+// MFMAs of the current one.
 // Rows past M (of dC) or K (of B) and columns past N read as zero, as the
 // reference's boundary-checked loads do.
 
@@ -25,7 +27,7 @@ extern "C" __attribute__((visibility("hidden"))) int void_internal_fail(int code
 namespace {
 
 constexpr int kT = 32;
-constexpr int kWavesPerBlock = 4;
+constexpr int kWaves = 4;  // waves per tile, each a quarter of the chunks of N
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -44,13 +46,14 @@ __device__ __forceinline__ uint32_t bf16_bits(float x) {
 // VEC: ldg, ldb and N multiples of 4 and 16-byte aligned operands, so a
 // 4-column group is either wholly inside N or wholly past it.
 template <int OUT, bool VEC>
-__global__ __launch_bounds__(64 * kWavesPerBlock) void sddmm_kernel(
+__global__ __launch_bounds__(64 * kWaves) void sddmm_kernel(
     const float* __restrict__ dC, int64_t ldg, const float* __restrict__ B, int64_t ldb,
     const int32_t* __restrict__ block_rows, const int32_t* __restrict__ block_cols, int32_t n_blocks, int32_t M,
     int32_t N, int32_t K, void* __restrict__ grad) {
+  __shared__ float part[kWaves][16][64];  // [wave][register][lane]: conflict-free writes and reads
   const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (t >= n_blocks) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t t = blockIdx.x;
   const int i = lane & 31, g = lane >> 5;
   const int br = block_rows[t], bc = block_cols[t];
   const int rx = br * kT + i, ry = bc * kT + i;
@@ -88,26 +91,42 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sddmm_kernel(
 #pragma unroll
     for (int s = 0; s < 16; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(c.x[s >> 2][s & 3], c.y[s >> 2][s & 3], acc, 0, 0, 0);
   };
-  Chunk X, Y;
-  load(X, 0);
-  for (int ch = 0;;) {
-    load(Y, ch + 1 < n_chunks ? ch + 1 : ch);  // unconditional: keeps the vmcnt waits exact
-    consume(X);
-    if (++ch >= n_chunks) break;
-    load(X, ch + 1 < n_chunks ? ch + 1 : ch);
-    consume(Y);
-    if (++ch >= n_chunks) break;
+  if (wave < n_chunks) {
+    // This wave's chunks: wave, wave + 4, ...; the next one is loaded
+    // unconditionally (past the end it re-reads the current one), which keeps
+    // the vmcnt waits exact.
+    Chunk X, Y;
+    load(X, wave);
+    for (int ch = wave;;) {
+      load(Y, ch + kWaves < n_chunks ? ch + kWaves : ch);
+      consume(X);
+      ch += kWaves;
+      if (ch >= n_chunks) break;
+      load(X, ch + kWaves < n_chunks ? ch + kWaves : ch);
+      consume(Y);
+      ch += kWaves;
+      if (ch >= n_chunks) break;
+    }
   }
-  // lane (j, g), register r: tile row 8 (r / 4) + 4 g + r % 4, tile column j
+#pragma unroll
+  for (int r = 0; r < 16; ++r) part[wave][r][lane] = acc[r];
+  __syncthreads();
+  // Wave w sums registers 4w .. 4w+3 over the four waves, in wave order, and
+  // stores them: lane (j, g), register r is tile row 8 (r / 4) + 4 g + r % 4,
+  // column j.
   const int j = lane & 31;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
+  for (int q = 0; q < 4; ++q) {
+    const int r = 4 * wave + q;
+    float v = part[0][r][lane];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) v += part[w][r][lane];
     const int row = 8 * (r >> 2) + 4 * g + (r & 3);
     const int64_t off = t * (kT * kT) + row * kT + j;
-    if constexpr (OUT == VOID_DT_F32) static_cast<float*>(grad)[off] = acc[r];
-    else if constexpr (OUT == VOID_DT_BF16) static_cast<uint16_t*>(grad)[off] = (uint16_t)bf16_bits(acc[r]);
+    if constexpr (OUT == VOID_DT_F32) static_cast<float*>(grad)[off] = v;
+    else if constexpr (OUT == VOID_DT_BF16) static_cast<uint16_t*>(grad)[off] = (uint16_t)bf16_bits(v);
     else {
-      _Float16 h = (_Float16)acc[r];
+      _Float16 h = (_Float16)v;
       uint16_t u;
       __builtin_memcpy(&u, &h, 2);
       static_cast<uint16_t*>(grad)[off] = u;
@@ -118,8 +137,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void sddmm_kernel(
 template <int OUT, bool VEC>
 int go(const float* dC, int64_t ldg, const float* B, int64_t ldb, const int32_t* rows, const int32_t* cols,
        int32_t n, int32_t M, int32_t N, int32_t K, void* grad, hipStream_t stream) {
-  const int grid = (n + kWavesPerBlock - 1) / kWavesPerBlock;
-  hipLaunchKernelGGL((sddmm_kernel<OUT, VEC>), dim3(grid), dim3(64 * kWavesPerBlock), 0, stream, dC, ldg, B, ldb, rows,
+  hipLaunchKernelGGL((sddmm_kernel<OUT, VEC>), dim3(n), dim3(64 * kWaves), 0, stream, dC, ldg, B, ldb, rows,
                      cols, n, M, N, K, grad);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return void_internal_fail(VOID_ERR_HIP, hipGetErrorString(e));
