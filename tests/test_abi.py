@@ -43,7 +43,11 @@ def _check_plan(row_ptr, col_idx, chunk):
     items, n_tiles, n_slots = _runtime.plan_rows(row_ptr, chunk, col_idx)
     covered = np.zeros(row_ptr[-1], dtype=np.int32)
     lengths = items[:, 2] - items[:, 1]
-    assert np.all(lengths[:-1] >= lengths[1:]), "items must be longest first"
+    # longest first; with split rows, dealt round-robin into 8 piles laid end to end
+    expect = np.sort(lengths)[::-1]
+    if np.any(items[:, 3] >= 0):
+        expect = np.concatenate([expect[p::8] for p in range(8)])
+    assert np.array_equal(lengths, expect), "items must be longest first (dealt into 8 piles when rows split)"
     tiles, slots = set(), set()
     for it in items:
         row, b, e, tile, nch, ch, slot = it[:7]
@@ -204,7 +208,8 @@ def test_analyze_workload_balance():
 
 def test_chunk_table():
     assert tuning.select_chunk("int8", 1638, 512) == 64                       # c2: no split
-    assert tuning.select_chunk("int8", 17960, 256) == 64                      # c4: capped at 64
+    assert tuning.select_chunk("int8", 17960, 256) == 64                      # rows of <= 64 tiles: no split
+    assert tuning.select_chunk("int8", 17960, 256, max_row=512) == 92         # c4: 1.3 x per-slot average
     assert tuning.n_panels(512) == 4 and tuning.n_panels(130) == 2
 
 

@@ -1891,10 +1891,26 @@ int void_streamk_plan(const int32_t* row_ptr, const int32_t* col_idx, int32_t n_
     tiles += 1;
     slots += nch;
   }
-  // Longest items first so that the tail of the dispatch is short ones.
+  // Longest items first so that the tail of the dispatch is short ones.  When
+  // rows were split (a long-tailed row distribution) the list is then dealt
+  // round-robin into 8 piles laid end to end: the kernels give each XCD a
+  // contiguous range of the work list (for L2 locality), and dealing makes
+  // every such range a balanced mix of long and short items, still longest
+  // first -- otherwise the first XCD receives all of the longest rows
+  // (measured on the power-law config: 84 us undealt, 56 us dealt).  With
+  // no split rows the lengths are close and dealing measured slower (c2:
+  // 12.0 us against 10.2 us), so the plain order is kept.
   std::stable_sort(out.begin(), out.end(), [](const void_work_item& x, const void_work_item& y) {
     return (x.end - x.begin) > (y.end - y.begin);
   });
+  if (tiles > 0) {
+    constexpr size_t kPiles = 8;
+    std::vector<void_work_item> dealt;
+    dealt.reserve(out.size());
+    for (size_t pile = 0; pile < kPiles; ++pile)
+      for (size_t i = pile; i < out.size(); i += kPiles) dealt.push_back(out[i]);
+    out.swap(dealt);
+  }
   *n_items = (int32_t)out.size();
   *n_split_tiles = tiles;
   *n_slots = slots;
