@@ -109,7 +109,7 @@ typedef struct void_plan {
 
 /* The dense operand and the output of one SpMM call. */
 typedef struct void_dense_args {
-  const void* b;          /* K x N int8 / e4m3fn */
+  const void* b;          /* K x N: int8 (void_spmm_int8), e4m3fn (void_spmm_fp8), fp32 (void_spmm_f32) */
   int64_t ldb;            /* elements between consecutive rows (row-major) or columns (column-major) */
   int32_t b_col_major;    /* 0: (k,n) at b[k*ldb+n]; 1: (k,n) at b[n*ldb+k] */
   int32_t N;
@@ -139,8 +139,11 @@ int void_panel_width(void);
 /* Host-side Stream-K planner.  Replaces compute_stream_k_workload
  * (void/stream_k.py:36-110): every block-row becomes one item, except rows
  * with more than chunk_tiles tiles, which are split into ceil(n/chunk_tiles)
- * near-equal chunks.  Items are ordered longest-first; empty rows are kept
- * (they produce the zero / activation(bias) rows of C).
+ * near-equal chunks.  Items are ordered longest-first -- when rows were
+ * split, that list is dealt round-robin into 8 piles laid end to end, so
+ * that the contiguous share of the list each XCD runs is a balanced mix --
+ * and empty rows are kept (they produce the zero / activation(bias) rows of
+ * C).
  * row_ptr (n_block_rows + 1 entries) and col_idx (row_ptr[n_block_rows]
  * entries, or NULL to leave cols[] at -1) are HOST arrays.
  * On VOID_ERR_CAPACITY, *n_items holds the required capacity. */
