@@ -44,8 +44,9 @@ from .fp8 import (
     void_spmm_fp8,
     void_tensor_to_fp8,
 )
-from .fusion import (ActivationType, FusedSparseLinear, get_activation_code, void_spmm_gelu, void_spmm_relu,
-                     void_spmm_silu)
+from .fusion import (ActivationType, FusedOpType, FusedSparseLinear, FusedSparseOp, create_fused_spmm_gelu,
+                     create_fused_spmm_relu, create_sparse_mlp, fused_sparse_mlp, get_activation_code, void_spmm_gelu,
+                     void_spmm_relu, void_spmm_silu)
 from .packed import load_packed, pack, save_packed, unpack
 from .ops import void_spmm
 from .autograd import SparseLinear, VOIDSpMM, VOIDSpMMFunction
