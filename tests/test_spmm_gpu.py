@@ -28,10 +28,11 @@ pytestmark = pytest.mark.gpu
 FP8_TOL = 2.0 ** -13
 
 
-@pytest.fixture(params=["cg", "bsr", "rg"])
+@pytest.fixture(params=["cg", "cgd", "bsr", "rg"])
 def kernel(request, monkeypatch):
-    """Runs a test on each SpMM kernel: the column-group kernel (forced with
-    VOID_AMD_KERNEL=cg; the default dispatch takes it for these shapes), the
+    """Runs a test on each SpMM kernel: the column-group kernel with its
+    LDS-DMA ring (=cgd, the default for row-major B; column-major B runs the
+    register-staged loop), the register-staged column-group loop (=cg), the
     general kernel (=bsr) and the row-grouped kernel (=rg, where its
     conditions hold; elsewhere the default dispatch runs)."""
     monkeypatch.setenv("VOID_AMD_KERNEL", request.param)

@@ -302,22 +302,33 @@ struct Accum<kEltFp8, EPI> {
   }
 };
 
+// sigmoid(t) = 1 / (1 + e^-t) = 1 / (1 + 2^(-t log2 e)) on the hardware
+// exp2 and reciprocal (1 ulp each).  Rounding -t log2 e costs |t| 2^-24 ln 2
+// relative error at most, where sigmoid is e^t-small; elsewhere it is
+// damped.  Saturates to exactly 1 and 0; NaN propagates.
+__device__ __forceinline__ float sigmoid_fast(float t) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t * -1.4426950408889634f));
+}
+
 __device__ __forceinline__ float activate(float x, int act) {
   if (act == VOID_ACT_RELU) return fmaxf(x, 0.0f);
   if (act == VOID_ACT_GELU) {
-    // fusion.py:38-43: inner = 0.7978845608 (x + 0.044715 x^3); tanh = 2 sigmoid(2 inner) - 1
+    // fusion.py:38-43: inner = 0.7978845608 (x + 0.044715 x^3) and
+    // 0.5 x (1 + tanh(inner)), with tanh(u) = 2 sigmoid(2u) - 1, which is
+    // x sigmoid(2 inner).
     const float inner = 0.7978845608f * (x + 0.044715f * x * x * x);
-    const float sig = 1.0f / (1.0f + expf(-2.0f * inner));
-    return x * 0.5f * (1.0f + (2.0f * sig - 1.0f));
+    return x * sigmoid_fast(2.0f * inner);
   }
-  if (act == VOID_ACT_SILU) return x * (1.0f / (1.0f + expf(-x)));
+  if (act == VOID_ACT_SILU) return x * sigmoid_fast(x);
   return x;
 }
 
+// gfx950's v_cvt_pk_bf16_f32: round to nearest even, NaN stays a (quiet) NaN.
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
-  const uint32_t u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;  // quiet NaN
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;                  // round to nearest even
+  const __bf16 h = (__bf16)x;
+  uint16_t u;
+  __builtin_memcpy(&u, &h, 2);
+  return u;
 }
 
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float x) {
@@ -853,8 +864,60 @@ struct CgBatch {
   int last_mask;       // bit u: tile u's slab is the one that crosses K
 };
 
-template <int ELT, int EPI, int OUT, bool BCOL>
+// LDS-DMA variant (DMA = true, row-major B only): the same work split and
+// LDS footprint, but the 16 tile slots form a ring of kDmaStages stages of
+// kDmaTiles tiles, filled by buffer loads that write LDS directly
+// (buffer_load_dwordx4 ... lds).  No batch is staged in registers, so three
+// stages (12 tiles) stay in flight while one is multiplied, against one batch
+// of 8 for the register-staged loop.  Each wave issues exactly 5 loads per
+// stage (its A tile and 8 rows of each of the 4 B slabs), so the wait for
+// stage s is vmcnt(5 x stages issued after s).
+constexpr int kDmaTiles = 4;
+constexpr int kDmaStages = 4;
+static_assert(kDmaTiles == kWaves, "one A tile per wave per stage");
+static_assert(kDmaTiles * kDmaStages == 2 * kCgBatch, "the ring reuses the register-staged loop's LDS");
+
+// The loads are inline asm, invisible to the compiler's wait insertion: given
+// the builtin, it cannot tell the ring's slots apart and waits for every
+// outstanding LDS load (vmcnt(0)) before each LDS read, which drains the
+// ring.  Invisible loads only ever make the compiler's own vmcnt waits
+// stricter (they return in order), so its waits stay correct; the ring's
+// waits are explicit.  The descriptor is a raw buffer (stride 0, 2^31 - 1
+// bytes) as make_rsrc builds, held in SGPRs.
+typedef int v4s __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4s sgpr_rsrc(const void* p) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  return v4s{__builtin_amdgcn_readfirstlane((int)(uint32_t)a), __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)),
+             0x7fffffff, 0x00020000};
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// 16 bytes per lane: lane l writes LDS bytes lds + 16 l .. + 15.
+__device__ __forceinline__ void dma_b128(v4s r, const void* lds, int voff, int soff) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+               :: "v"(voff), "s"(r), "s"(soff), "{m0}"(lds_addr(lds)) : "memory");
+}
+
+// 4 bytes per lane: lane l writes LDS bytes lds + 4 l .. + 3.
+__device__ __forceinline__ void dma_b32(v4s r, const void* lds, int voff, int soff) {
+  asm volatile("buffer_load_dword %0, %1, %2 offen lds"
+               :: "v"(voff), "s"(r), "s"(soff), "{m0}"(lds_addr(lds)) : "memory");
+}
+
+// s_waitcnt vmcnt(n), also a compiler barrier for memory accesses (the
+// builtin is not one: LDS reads could move above it).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void spmm_cg_kernel(Params p) {
+  static_assert(!(DMA && BCOL), "the LDS-DMA ring is for row-major B");
   using A = Accum1<ELT, EPI>;
   constexpr bool kInt = A::kInt;
   constexpr bool kScales = (EPI == VOID_EPI_PER_BLOCK);
@@ -1007,7 +1070,89 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
   };
 
-  if (nt > 0) {
+  if constexpr (DMA) {
+    v4i(*a_ring)[64] = &a_lds[0][0];
+    uint8_t(*b_ring)[kSlotBytes] = &b_lds[0][0];
+    const v4s da = sgpr_rsrc(p.tiles), db = sgpr_rsrc(p.b), dcol = sgpr_rsrc(p.col_idx), dsc = sgpr_rsrc(p.a_scale);
+    // Each wave's own copy of the item's block columns and scales (one per
+    // lane), parked in the B area of the last stage's first slot until the
+    // first stage has landed: that slot is first refilled after the barrier
+    // of stage 0, when every wave has read its copy back.
+    int* win = reinterpret_cast<int*>(&b_ring[(kDmaStages - 1) * kDmaTiles][wave * 512]);
+    if (nt > 0) {
+      const int ci = begin + min(lane, nt - 1);
+      dma_b32(dcol, win, ci * 4, 0);
+      if constexpr (kScales) dma_b32(dsc, win + 64, p.per_tensor_a ? 0 : ci * 4, 0);
+    }
+    // Lane (row brow, 16-byte position lane & 7) of a slab receives global
+    // chunk (lane & 7) ^ (brow & 7): the XOR swizzle read_tr expects.  Rows
+    // past K in the slab that crosses K load nothing (out of range).
+    int cbd = panel * kPanel + 16 * ((lane & 7) ^ (brow & 7));
+    cbd = cbd < p.N ? cbd : 0;  // past N: any valid 16 bytes, never stored
+    const int voffd = (int)(brow * p.ldb) + cbd;
+    const int voffd_last = (kb_last < 0 || brow < p.K - kb_last * kTile) ? voffd : kOutOfRange;
+    const int ns = (nt + kDmaTiles - 1) / kDmaTiles;
+    auto stage_col = [&](int s, int u) -> int {
+      const int t = s * kDmaTiles + u;
+      int kb;
+      if (s < 4) {
+        const v4i c = s == 0 ? cq0 : s == 1 ? cq1 : s == 2 ? cq2 : cq3;
+        kb = c[u];
+        kb = kb >= 0 ? kb : max(cq0[0], 0);
+      } else {
+        kb = __builtin_amdgcn_readlane(colw, min(t, kCgMaxTiles - 1));
+      }
+      return __builtin_amdgcn_readfirstlane(kb);
+    };
+    auto issue_stage = [&](int s) {
+      const int slot0 = (s % kDmaStages) * kDmaTiles;
+      const int base = s * kDmaTiles;
+      const int idx = base + wave;
+      const bool live = idx < nt;
+      dma_b128(da, &a_ring[slot0 + wave][0], live ? voff_a : kOutOfRange, (begin + (live ? idx : 0)) * (kTile * kTile));
+#pragma unroll
+      for (int u = 0; u < kDmaTiles; ++u) {
+        const int kb = stage_col(s, u);
+        const int vo = base + u < nt ? (kb == kb_last ? voffd_last : voffd) : kOutOfRange;
+        dma_b128(db, &b_ring[slot0 + u][wave * (kSlotBytes / kWaves)], vo, kb * b_kstride);
+      }
+    };
+#pragma unroll
+    for (int s = 0; s < kDmaStages - 1; ++s)
+      if (s < ns) issue_stage(s);
+    TRACE_POINT(1);
+    for (int s = 0; s < ns; ++s) {
+      const int ahead = min(ns - 1, s + kDmaStages - 2) - s;  // stages issued after s
+      if (ahead >= 2) wait_vm<2 * (1 + kDmaTiles)>();
+      else if (ahead == 1) wait_vm<1 + kDmaTiles>();
+      else wait_vm<0>();
+      if (s == 0) {
+        // The windows were issued before stage 0, so they have landed too.
+        colw = win[lane];
+        if constexpr (kScales) scw = __int_as_float(win[64 + lane]);
+        TRACE_POINT(5);
+      }
+      // Every wave's part of stage s has landed, and every wave has finished
+      // reading stage s - 1, whose slots the next issue overwrites.
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (s + kDmaStages - 1 < ns) issue_stage(s + kDmaStages - 1);
+      const int slot0 = (s % kDmaStages) * kDmaTiles;
+      const int base = s * kDmaTiles;
+#pragma unroll
+      for (int u = 0; u < kDmaTiles; ++u) {
+        if (base + u < nt) {
+          Frag1 f;
+          f.a = a_ring[slot0 + u][lane];
+          f.b = read_tr(&b_ring[slot0 + u][0], wave, j, g);
+          float sc = 0.f;
+          if constexpr (kScales) sc = bcast(scw, base + u);
+          A::step(acc, f, sc);
+        }
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    TRACE_POINT(6);
+  } else if (nt > 0) {
     {
       const int ci = begin + min(lane, nt - 1);
       colw = __builtin_amdgcn_raw_buffer_load_b32(rcol, ci * 4, 0, 0);
@@ -1110,6 +1255,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int voff_c = ((4 * g) * ldc + col) * esz;
   const int row0 = row * kTile;
   const bool full = row0 + kTile <= p.M && cg * kTile + kTile <= p.N;
+  // Each store instruction writes one full 32-column row segment per half
+  // wave (128 bytes for f32).
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int rr = 8 * (r >> 2) + (r & 3);
@@ -1135,9 +1282,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   TRACE_FLUSH();
 }
 
-template <int ELT, int EPI, int OUT, bool BCOL>
+template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false>
 int launch_cg(const Params& p, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((spmm_cg_kernel<ELT, EPI, OUT, BCOL>), dim3(grid), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((spmm_cg_kernel<ELT, EPI, OUT, BCOL, DMA>), dim3(grid), dim3(kThreads), 0, stream, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(VOID_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
   return VOID_OK;
@@ -1734,8 +1881,9 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
 
   // The column-group and row-grouped kernels address every operand with
   // 31-bit buffer offsets; larger operands and the other B layouts use
-  // spmm_bsr_kernel.  VOID_AMD_KERNEL=bsr / cg / rg forces a kernel where
-  // it applies (for comparisons and tests).
+  // spmm_bsr_kernel.  VOID_AMD_KERNEL=bsr / cg / cgd / rg forces a kernel
+  // where it applies (for comparisons and tests; cg is the register-staged
+  // column-group loop, cgd its LDS-DMA ring, the default).
   const int esz = (d->out_dtype == VOID_DT_BF16 || d->out_dtype == VOID_DT_F16) ? 2 : 4;
   const int64_t kLim = (int64_t)1 << 31;
   const int64_t b_span = d->b_col_major ? (int64_t)d->N * d->ldb
@@ -1786,22 +1934,23 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
                      !force_bsr;
   if (cg_ok) {
     const bool bcol = layout == kColVec;
+    // Row-major B takes the LDS-DMA ring unless VOID_AMD_KERNEL=cg asks for
+    // the register-staged loop.
+    const bool dma = !bcol && !force_cg;
     auto go = [&](auto elt_c, auto epi_c) -> int {
       constexpr int E = decltype(elt_c)::value, P = decltype(epi_c)::value;
+      auto pick = [&](auto out_c) -> int {
+        constexpr int O = decltype(out_c)::value;
+        if (bcol) return launch_cg<E, P, O, true>(p, grid, stream);
+        return dma ? launch_cg<E, P, O, false, true>(p, grid, stream) : launch_cg<E, P, O, false>(p, grid, stream);
+      };
       if constexpr (P == VOID_EPI_RAW_I32) {
-        return bcol ? launch_cg<E, P, VOID_DT_I32, true>(p, grid, stream)
-                    : launch_cg<E, P, VOID_DT_I32, false>(p, grid, stream);
+        return pick(std::integral_constant<int, VOID_DT_I32>{});
       } else {
         switch (d->out_dtype) {
-          case VOID_DT_F32:
-            return bcol ? launch_cg<E, P, VOID_DT_F32, true>(p, grid, stream)
-                        : launch_cg<E, P, VOID_DT_F32, false>(p, grid, stream);
-          case VOID_DT_BF16:
-            return bcol ? launch_cg<E, P, VOID_DT_BF16, true>(p, grid, stream)
-                        : launch_cg<E, P, VOID_DT_BF16, false>(p, grid, stream);
-          case VOID_DT_F16:
-            return bcol ? launch_cg<E, P, VOID_DT_F16, true>(p, grid, stream)
-                        : launch_cg<E, P, VOID_DT_F16, false>(p, grid, stream);
+          case VOID_DT_F32: return pick(std::integral_constant<int, VOID_DT_F32>{});
+          case VOID_DT_BF16: return pick(std::integral_constant<int, VOID_DT_BF16>{});
+          case VOID_DT_F16: return pick(std::integral_constant<int, VOID_DT_F16>{});
           default:
             return fail(VOID_ERR_UNSUPPORTED, "out_dtype %d not supported with this epilogue", d->out_dtype);
         }
