@@ -832,6 +832,19 @@ template <int EPI>
 struct Accum1<kEltI8, EPI> {
   static constexpr bool kInt = (EPI != VOID_EPI_PER_BLOCK);
   using Reg = typename std::conditional<kInt, v16i, v16f>::type;
+  using Part = v16i;
+  // Per-block epilogue split in two, so that products of several tiles can
+  // be in flight before their scaled adds.
+  __device__ __forceinline__ static Part prod(const Frag1& f) {
+    const v16i z = {};
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a, f.b, z, 0, 0, 0);
+  }
+  __device__ __forceinline__ static void fold(Reg& acc, const Part& part, float s) {
+    if constexpr (!kInt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = __builtin_fmaf(s, (float)part[r], acc[r]);
+    }
+  }
   __device__ __forceinline__ static void step(Reg& acc, const Frag1& f, float s) {
     if constexpr (kInt) {
       acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a, f.b, acc, 0, 0, 0);
@@ -848,6 +861,16 @@ template <int EPI>
 struct Accum1<kEltFp8, EPI> {
   static constexpr bool kInt = false;
   using Reg = v16f;
+  using Part = v16f;
+  __device__ __forceinline__ static Part prod(const Frag1& f) {
+    const v16f z = {};
+    v16f part = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(pack2(f.a[0], f.a[1]), pack2(f.b[0], f.b[1]), z, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(pack2(f.a[2], f.a[3]), pack2(f.b[2], f.b[3]), part, 0, 0, 0);
+  }
+  __device__ __forceinline__ static void fold(Reg& acc, const Part& part, float s) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = __builtin_fmaf(s, part[r], acc[r]);
+  }
   __device__ __forceinline__ static void step(Reg& acc, const Frag1& f, float s) {
     const v16f z = {};
     v16f part = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(pack2(f.a[0], f.a[1]), pack2(f.b[0], f.b[1]), z, 0, 0, 0);
@@ -1138,15 +1161,40 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       if (s + kDmaStages - 1 < ns) issue_stage(s + kDmaStages - 1);
       const int slot0 = (s % kDmaStages) * kDmaTiles;
       const int base = s * kDmaTiles;
+      if (base + kDmaTiles <= nt) {
+        // A full stage: all operand reads first, then four independent
+        // products, so that one tile's scaling overlaps the next MFMA.
+        Frag1 f[kDmaTiles];
 #pragma unroll
-      for (int u = 0; u < kDmaTiles; ++u) {
-        if (base + u < nt) {
-          Frag1 f;
-          f.a = a_ring[slot0 + u][lane];
-          f.b = read_tr(&b_ring[slot0 + u][0], wave, j, g);
-          float sc = 0.f;
-          if constexpr (kScales) sc = bcast(scw, base + u);
-          A::step(acc, f, sc);
+        for (int u = 0; u < kDmaTiles; ++u) {
+          f[u].a = a_ring[slot0 + u][lane];
+          f[u].b = read_tr(&b_ring[slot0 + u][0], wave, j, g);
+        }
+        if constexpr (kInt) {
+#pragma unroll
+          for (int u = 0; u < kDmaTiles; ++u) A::step(acc, f[u], 0.f);
+        } else {
+          // Products two tiles ahead of their scaled adds: the VALU work of
+          // tile u runs while the MFMA of tile u + 2 executes.
+          typename A::Part part[kDmaTiles];
+          part[0] = A::prod(f[0]);
+          part[1] = A::prod(f[1]);
+#pragma unroll
+          for (int u = 0; u < kDmaTiles; ++u) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (u + 2 < kDmaTiles) part[u + 2] = A::prod(f[u + 2]);
+            A::fold(acc, part[u], bcast(scw, base + u));
+          }
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < kDmaTiles; ++u) {
+          if (base + u < nt) {
+            Frag1 f;
+            f.a = a_ring[slot0 + u][lane];
+            f.b = read_tr(&b_ring[slot0 + u][0], wave, j, g);
+            A::step(acc, f, kScales ? bcast(scw, base + u) : 0.f);
+          }
         }
       }
     }
