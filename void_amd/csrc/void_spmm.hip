@@ -1303,6 +1303,43 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int voff_c = ((4 * g) * ldc + col) * esz;
   const int row0 = row * kTile;
   const bool full = row0 + kTile <= p.M && cg * kTile + kTile <= p.N;
+  // LDS-DMA variant, whole block in range and 16-byte aligned rows: the
+  // wave's 32 x 32 block goes through its own row-major LDS area (the B ring
+  // is idle after the loop's last barrier) and leaves as 16-byte stores,
+  // each covering 8 (f32, i32) or 16 (bf16, f16) full 32-column row
+  // segments: 4 or 2 store instructions per lane in place of 16.
+  if constexpr (DMA) {
+    const bool vec = full && ((reinterpret_cast<uintptr_t>(p.c) | (uintptr_t)(ldc * esz)) & 15) == 0;
+    if (vec) {
+      constexpr int kRowB = kTile * esz + 16;  // padded row stride: the two half waves hit other banks
+      uint8_t* stg = &b_lds[0][0][0] + wave * (kTile * kRowB);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rr = 8 * (r >> 2) + (r & 3) + 4 * g;
+        float x;
+        if constexpr (EPI == VOID_EPI_ROW_MEAN || EPI == VOID_EPI_PER_BLOCK) x = __fmul_rn((float)acc[r], mul);
+        else x = 0.f;
+        if (p.bias) x = __fadd_rn(x, bias);
+        x = activate(x, p.activation);
+        uint8_t* d = stg + rr * kRowB + j * esz;
+        if constexpr (OUT == VOID_DT_F32) *reinterpret_cast<float*>(d) = x;
+        else if constexpr (OUT == VOID_DT_I32) *reinterpret_cast<int*>(d) = (int)acc[r];
+        else *reinterpret_cast<uint16_t*>(d) = (uint16_t)(OUT == VOID_DT_BF16 ? f32_to_bf16_bits(x) : f32_to_f16_bits(x));
+      }
+      constexpr int kChunks = kTile * esz / 16;  // 16-byte chunks per row segment
+      constexpr int kRowsPer = 64 / kChunks;     // rows per store instruction
+      const int ch = lane % kChunks;
+#pragma unroll
+      for (int k = 0; k < kTile / kRowsPer; ++k) {
+        const int rw = k * kRowsPer + lane / kChunks;
+        const v4i v = *reinterpret_cast<const v4i*>(stg + rw * kRowB + ch * 16);
+        __builtin_amdgcn_raw_buffer_store_b128(v, rc, ((row0 + rw) * ldc + cg * kTile) * esz + ch * 16, 0, 0);
+      }
+      TRACE_POINT(4);
+      TRACE_FLUSH();
+      return;
+    }
+  }
   // Each store instruction writes one full 32-column row segment per half
   // wave (128 bytes for f32).
 #pragma unroll
