@@ -895,6 +895,10 @@ struct CgBatch {
 // of 8 for the register-staged loop.  Each wave issues exactly 5 loads per
 // stage (its A tile and 8 rows of each of the 4 B slabs), so the wait for
 // stage s is vmcnt(5 x stages issued after s).
+// Cache policy of the staged C stores: nt | sc1 (non-temporal, agent
+// scope).  C is written once and not read by the kernel; on c2 this measured
+// 8.7 us cold / 7.2 us hot against 9.2-9.3 / 8.0 with the default policy.
+constexpr int kStoreStream = 2 | 16;
 constexpr int kDmaTiles = 4;
 constexpr int kDmaStages = 4;
 static_assert(kDmaTiles == kWaves, "one A tile per wave per stage");
@@ -1333,7 +1337,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int k = 0; k < kTile / kRowsPer; ++k) {
         const int rw = k * kRowsPer + lane / kChunks;
         const v4i v = *reinterpret_cast<const v4i*>(stg + rw * kRowB + ch * 16);
-        __builtin_amdgcn_raw_buffer_store_b128(v, rc, ((row0 + rw) * ldc + cg * kTile) * esz + ch * 16, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(v, rc, ((row0 + rw) * ldc + cg * kTile) * esz + ch * 16, 0, kStoreStream);
       }
       TRACE_POINT(4);
       TRACE_FLUSH();
