@@ -140,8 +140,9 @@ def time_gpu(prob, steps: int, warmup: int, flush: bool):
     """Kernel time from HIP-graph replays, so host launch overhead is excluded.
 
     cold: a graph of `steps` x (overwrite a 1 GiB buffer, SpMM) minus a graph of
-    `steps` x (overwrite) -- the SpMM then always starts with L2 and the
-    Infinity Cache holding none of its inputs; hot: a graph of `steps` x SpMM.
+    `steps` x (overwrite), median over 7 alternating pairs of replays -- the
+    SpMM then always starts with L2 and the Infinity Cache holding none of its
+    inputs; hot: a graph of `steps` x SpMM.
     Both graphs are bracketed by events on the capture-replay stream with a
     device synchronisation on either side.
     """
@@ -181,7 +182,16 @@ def time_gpu(prob, steps: int, warmup: int, flush: bool):
     if flush:
         g_cold = capture(cold_body)
         g_flush = capture(lambda i: scratch.fill_(float(i)))
-        cold = (replay_ms(g_cold) - replay_ms(g_flush)) / steps
+        g_cold.replay()
+        g_flush.replay()
+        torch.cuda.synchronize()
+        # Replays of the two graphs alternate and the median of the pairwise
+        # differences is kept: the overwrites take ~15x the SpMM, so drift in
+        # their speed between two separate averages would swamp the result.
+        diffs = []
+        for _ in range(7):
+            diffs.append(replay_ms(g_cold, reps=1) - replay_ms(g_flush, reps=1))
+        cold = sorted(diffs)[len(diffs) // 2] / steps
     wall = time.perf_counter() - t0
     return cold, hot, wall
 
