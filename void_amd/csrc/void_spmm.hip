@@ -887,22 +887,27 @@ struct CgBatch {
   int last_mask;       // bit u: tile u's slab is the one that crosses K
 };
 
-// LDS-DMA variant (DMA = true, row-major B only): the same work split and
-// LDS footprint, but the 16 tile slots form a ring of kDmaStages stages of
-// kDmaTiles tiles, filled by buffer loads that write LDS directly
-// (buffer_load_dwordx4 ... lds).  No batch is staged in registers, so three
-// stages (12 tiles) stay in flight while one is multiplied, against one batch
-// of 8 for the register-staged loop.  Each wave issues exactly 5 loads per
-// stage (its A tile and 8 rows of each of the 4 B slabs), so the wait for
-// stage s is vmcnt(5 x stages issued after s).
+// LDS-DMA variant (DMA = true, row-major B only): the same work split, but
+// the tile slots form a ring of kDmaStages stages of kDmaTiles tiles, filled
+// by buffer loads that write LDS directly (buffer_load_dwordx4 ... lds), so
+// no batch is staged in registers.  Two stages (40 KB) and about 100 VGPRs
+// let four workgroups (16 waves) share a CU; one workgroup's record fetch,
+// stage waits and epilogue then overlap the others' MFMA work.  Measured
+// against deeper rings at lower occupancy (4 stages with 2 workgroups per
+// CU, 2-tile stages with 4-6 workgroups), this was fastest on c2, c3 and c5.
+// A wave issues kDmaTiles B loads per stage (8 rows of each slab), and the
+// first kDmaTiles waves one A tile each, so the wait for stage s is vmcnt of
+// that count times the stages issued after s.
+constexpr int kDmaTiles = 4;
+constexpr int kDmaStages = 2;
+constexpr int kDmaWavesPerEu = 4;  // workgroups per CU, as LDS (4 x 40 KB) allows
+static_assert(kDmaTiles <= kWaves, "at most one A tile per wave per stage");
+static_assert(kDmaStages >= 2 && kDmaStages <= 4, "stage waits cover up to two stages ahead");
+
 // Cache policy of the staged C stores: nt | sc1 (non-temporal, agent
 // scope).  C is written once and not read by the kernel; on c2 this measured
 // 8.7 us cold / 7.2 us hot against 9.2-9.3 / 8.0 with the default policy.
 constexpr int kStoreStream = 2 | 16;
-constexpr int kDmaTiles = 4;
-constexpr int kDmaStages = 4;
-static_assert(kDmaTiles == kWaves, "one A tile per wave per stage");
-static_assert(kDmaTiles * kDmaStages == 2 * kCgBatch, "the ring reuses the register-staged loop's LDS");
 
 // The loads are inline asm, invisible to the compiler's wait insertion: given
 // the builtin, it cannot tell the ring's slots apart and waits for every
@@ -942,18 +947,29 @@ __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
 }
 
+// Wait until at most `ahead` stages of C loads each are outstanding.
+template <int C>
+__device__ __forceinline__ void wait_stages(int ahead) {
+  if (ahead >= 2) wait_vm<2 * C>();
+  else if (ahead == 1) wait_vm<C>();
+  else wait_vm<0>();
+}
+
 template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void spmm_cg_kernel(Params p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? kDmaWavesPerEu : 2, DMA ? kDmaWavesPerEu : 2))) void spmm_cg_kernel(Params p) {
   static_assert(!(DMA && BCOL), "the LDS-DMA ring is for row-major B");
   using A = Accum1<ELT, EPI>;
   constexpr bool kInt = A::kInt;
   constexpr bool kScales = (EPI == VOID_EPI_PER_BLOCK);
 
-  __shared__ __attribute__((aligned(16))) v4i a_lds[2][kCgBatch][64];
-  __shared__ __attribute__((aligned(16))) uint8_t b_lds[BCOL ? 1 : 2][BCOL ? 1 : kCgBatch][BCOL ? 16 : kSlotBytes];
+  // Tile slots: two batches of the register-staged loop, or the LDS-DMA ring.
+  constexpr int kSlots = DMA ? kDmaStages * kDmaTiles : 2 * kCgBatch;
+  __shared__ __attribute__((aligned(16))) v4i a_lds[kSlots][64];
+  __shared__ __attribute__((aligned(16))) uint8_t b_lds[BCOL ? 1 : kSlots][BCOL ? 16 : kSlotBytes];
   // Split-row arrival flag: the first word of the A area, free once every
-  // wave has passed the tile loop (80 KB in total keeps two workgroups per CU).
-  int& s_last = *reinterpret_cast<int*>(&a_lds[0][0][0]);
+  // wave has passed the tile loop (no LDS word is spare: 80 KB keeps the
+  // register-staged loop at two workgroups per CU, 40 KB the ring at four).
+  int& s_last = *reinterpret_cast<int*>(&a_lds[0][0]);
 
   TRACE_DECL;
   const int tid = threadIdx.x;
@@ -1069,7 +1085,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int base = bb * kCgBatch;
     const int buf = bb & 1;
 #pragma unroll
-    for (int q = 0; q < kCgAPerWave; ++q) a_lds[buf][wave + kWaves * q][lane] = x.a[q];
+    for (int q = 0; q < kCgAPerWave; ++q) a_lds[buf * kCgBatch + wave + kWaves * q][lane] = x.a[q];
     if constexpr (!BCOL) {
 #pragma unroll
       for (int u = 0; u < kCgBatch; ++u) {
@@ -1079,7 +1095,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
           // NaN, and NaN times the zero padding of A is still NaN.
           if (((x.last_mask >> u) & 1) && brow >= p.K - kb_last * kTile) v = v4i{0, 0, 0, 0};
         }
-        *reinterpret_cast<v4i*>(&b_lds[buf][u][brow * kPanel + (((lane & 7) ^ (brow & 7)) << 4)]) = v;
+        *reinterpret_cast<v4i*>(&b_lds[buf * kCgBatch + u][brow * kPanel + (((lane & 7) ^ (brow & 7)) << 4)]) = v;
       }
     }
     __syncthreads();
@@ -1087,9 +1103,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int u = 0; u < kCgBatch; ++u) {
       if (base + u < nt) {
         Frag1 f;
-        f.a = a_lds[buf][u][lane];
+        f.a = a_lds[buf * kCgBatch + u][lane];
         if constexpr (BCOL) f.b = x.b[u];
-        else f.b = read_tr(&b_lds[buf][u][0], wave, j, g);
+        else f.b = read_tr(&b_lds[buf * kCgBatch + u][0], wave, j, g);
         float s = 0.f;
         if constexpr (kScales) s = bcast(scw, base + u);
         A::step(acc, f, s);
@@ -1098,8 +1114,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   };
 
   if constexpr (DMA) {
-    v4i(*a_ring)[64] = &a_lds[0][0];
-    uint8_t(*b_ring)[kSlotBytes] = &b_lds[0][0];
+    v4i(*a_ring)[64] = a_lds;
+    uint8_t(*b_ring)[kSlotBytes] = b_lds;
     const v4s da = sgpr_rsrc(p.tiles), db = sgpr_rsrc(p.b), dcol = sgpr_rsrc(p.col_idx), dsc = sgpr_rsrc(p.a_scale);
     // Each wave's own copy of the item's block columns and scales (one per
     // lane), parked in the B area of the last stage's first slot until the
@@ -1119,12 +1135,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int voffd = (int)(brow * p.ldb) + cbd;
     const int voffd_last = (kb_last < 0 || brow < p.K - kb_last * kTile) ? voffd : kOutOfRange;
     const int ns = (nt + kDmaTiles - 1) / kDmaTiles;
+    // The first kDmaTiles waves also load one A tile per stage.
+    const bool a_wave = wave < kDmaTiles;
     auto stage_col = [&](int s, int u) -> int {
       const int t = s * kDmaTiles + u;
       int kb;
-      if (s < 4) {
-        const v4i c = s == 0 ? cq0 : s == 1 ? cq1 : s == 2 ? cq2 : cq3;
-        kb = c[u];
+      if (t < 16) {
+        // Selects, not a dynamic vector index (that would go through scratch).
+        const int q = t >> 2, e = t & 3;
+        const v4i c = q == 0 ? cq0 : q == 1 ? cq1 : q == 2 ? cq2 : cq3;
+        kb = e == 0 ? c[0] : e == 1 ? c[1] : e == 2 ? c[2] : c[3];
         kb = kb >= 0 ? kb : max(cq0[0], 0);
       } else {
         kb = __builtin_amdgcn_readlane(colw, min(t, kCgMaxTiles - 1));
@@ -1134,9 +1154,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     auto issue_stage = [&](int s) {
       const int slot0 = (s % kDmaStages) * kDmaTiles;
       const int base = s * kDmaTiles;
-      const int idx = base + wave;
-      const bool live = idx < nt;
-      dma_b128(da, &a_ring[slot0 + wave][0], live ? voff_a : kOutOfRange, (begin + (live ? idx : 0)) * (kTile * kTile));
+      if (a_wave) {
+        const int idx = base + wave;
+        const bool live = idx < nt;
+        dma_b128(da, &a_ring[slot0 + wave][0], live ? voff_a : kOutOfRange,
+                 (begin + (live ? idx : 0)) * (kTile * kTile));
+      }
 #pragma unroll
       for (int u = 0; u < kDmaTiles; ++u) {
         const int kb = stage_col(s, u);
@@ -1150,9 +1173,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     TRACE_POINT(1);
     for (int s = 0; s < ns; ++s) {
       const int ahead = min(ns - 1, s + kDmaStages - 2) - s;  // stages issued after s
-      if (ahead >= 2) wait_vm<2 * (1 + kDmaTiles)>();
-      else if (ahead == 1) wait_vm<1 + kDmaTiles>();
-      else wait_vm<0>();
+      if (a_wave) wait_stages<1 + kDmaTiles>(ahead);
+      else wait_stages<kDmaTiles>(ahead);
       if (s == 0) {
         // The windows were issued before stage 0, so they have landed too.
         colw = win[lane];
@@ -1316,7 +1338,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const bool vec = full && ((reinterpret_cast<uintptr_t>(p.c) | (uintptr_t)(ldc * esz)) & 15) == 0;
     if (vec) {
       constexpr int kRowB = kTile * esz + 16;  // padded row stride: the two half waves hit other banks
-      uint8_t* stg = &b_lds[0][0][0] + wave * (kTile * kRowB);
+      uint8_t* stg = &b_lds[0][0] + wave * (kTile * kRowB);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int rr = 8 * (r >> 2) + (r & 3) + 4 * g;
