@@ -1271,14 +1271,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
     // stores, count arrivals per (row, panel), and let the last chunk read
     // every partial back with agent-coherent loads and reduce them in chunk
     // order, so the result does not depend on timing.
+    // Partial blocks: register 4 q + e of lane l at dword (q * 64 + l) * 4 + e
+    // of the wave's 4 KB block, so that each 16-byte store or load
+    // instruction covers 1 KB contiguously.  sc1 makes them agent-coherent
+    // (L2), as relaxed agent-scope atomics would be.
+    constexpr int kSc1 = 16;
     const int nchunks = itp->nchunks, slot = itp->slot, chunk = itp->chunk;
     constexpr size_t kBlock = (size_t)kTile * kTile;  // one wave's block
     int* part = static_cast<int*>(p.partials);
-    const size_t mine = (((size_t)(slot + chunk) * p.n_panels + panel) * kWaves + wave) * kBlock + lane * 16;
+    auto block_of = [&](int c) -> const int* {
+      return part + (((size_t)(slot + c) * p.n_panels + panel) * kWaves + wave) * kBlock;
+    };
+    {
+      const Rsrc rp = make_rsrc(block_of(chunk));
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int w = kInt ? (int)acc[r] : __float_as_int((float)acc[r]);
-      __hip_atomic_store(part + mine + r, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int q = 0; q < 4; ++q) {
+        v4i w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = kInt ? (int)acc[4 * q + e] : __float_as_int((float)acc[4 * q + e]);
+        __builtin_amdgcn_raw_buffer_store_b128(w, rp, (q * 64 + lane) * 16, 0, kSc1);
+      }
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are acknowledged
     __syncthreads();
@@ -1293,14 +1305,29 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
       return;
     }
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Reduce in chunk order (deterministic), with the loads of four chunks
+    // in flight at a time.
     typename A::Reg sum = {};
-    for (int ch = 0; ch < nchunks; ++ch) {
-      const size_t off = (((size_t)(slot + ch) * p.n_panels + panel) * kWaves + wave) * kBlock + lane * 16;
+    for (int c0 = 0; c0 < nchunks; c0 += 4) {
+      v4i x[4][4];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int x = __hip_atomic_load(part + off + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if constexpr (kInt) sum[r] += x;
-        else sum[r] += __int_as_float(x);
+      for (int k = 0; k < 4; ++k) {
+        const bool live = c0 + k < nchunks;
+        const Rsrc rp = make_rsrc(block_of(live ? c0 + k : c0));
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          x[k][q] = __builtin_amdgcn_raw_buffer_load_b128(rp, live ? (q * 64 + lane) * 16 : kOutOfRange, 0, kSc1);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (c0 + k < nchunks) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int v = x[k][r >> 2][r & 3];
+            if constexpr (kInt) sum[r] += v;
+            else sum[r] += __int_as_float(v);
+          }
+        }
       }
     }
     acc = sum;
