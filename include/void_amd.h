@@ -207,11 +207,13 @@ int void_quantize_tiles_fp8(const float* tiles, int32_t n_tiles, uint8_t* q, flo
  * entries; float32 values; indices and values 16-byte aligned) becomes Morton-ordered 32x32 fp32 tiles, block
  * rows, block columns and Morton codes, the reference's VOIDTensor fields.
  * Explicit zeros activate their tile, as in the reference.  Two calls:
- * void_csr_count_blocks writes the number of active blocks to *n_blocks (a
- * device int64), the caller sizes the outputs from it, then
- * void_csr_to_tiles fills them.  Both use the same workspace of
- * void_csr_workspace_bytes(M, N) bytes (0 when the block grid is too large
- * for the device conversion: more than 2^28 blocks). */
+ * void_csr_count_blocks flags the active blocks, ranks them in Morton order
+ * and writes their number to *n_blocks (a device int64); the caller sizes the
+ * outputs from it (the tile array 16-byte aligned), then void_csr_to_tiles
+ * fills them.  Both use the same workspace of void_csr_workspace_bytes(M, N)
+ * bytes, which carries the flags and ranks from the first call to the second
+ * (0 when the block grid is too large for the device conversion: more than
+ * 2^28 blocks). */
 size_t void_csr_workspace_bytes(int32_t M, int32_t N);
 int void_csr_count_blocks(const int32_t* indptr, const int32_t* indices, int32_t M, int32_t N, void* workspace,
                           size_t workspace_bytes, int64_t* n_blocks, hipStream_t stream);

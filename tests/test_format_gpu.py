@@ -7,6 +7,7 @@ import scipy.sparse as sp
 import torch
 
 import cases
+import oracle
 import void_amd
 
 pytestmark = pytest.mark.gpu
@@ -22,10 +23,21 @@ def _same(dev_vt, host_vt):
         assert torch.equal(a, b), name
 
 
+# Morton code spaces up to 32768 codes rank in one workgroup; the last two
+# shapes (65536 and 2^20 codes) take the chunked count / scan / rank path.
 @pytest.mark.parametrize("M,N,density,seed", [(300, 200, 0.05, 1), (2000, 70, 0.02, 2), (70, 3000, 0.02, 3),
-                                              (4096, 4096, 0.002, 4), (33, 33, 0.5, 5), (1, 1000, 0.1, 6)])
+                                              (4096, 4096, 0.002, 4), (33, 33, 0.5, 5), (1, 1000, 0.1, 6),
+                                              (8192, 6000, 0.0005, 7), (20000, 64, 0.01, 8)])
 def test_device_csr_to_void_matches_host(gpu, M, N, density, seed):
     A = sp.random(M, N, density=density, format="csr", random_state=seed, dtype=np.float64)
+    A.sort_indices()
+    _same(void_amd.csr_to_void(A, device="cuda"), void_amd.csr_to_void(A))
+
+
+def test_device_csr_dense_blocks(gpu):
+    # Fully dense tiles: every aligned run of four columns is one 16-byte store.
+    case = cases.uniform_blocks(2048, 3072, 64, 400, seed=9)
+    A = sp.csr_matrix(oracle.densify(case.tiles, case.block_rows, case.block_cols, (case.M, case.K)))
     A.sort_indices()
     _same(void_amd.csr_to_void(A, device="cuda"), void_amd.csr_to_void(A))
 
