@@ -928,16 +928,17 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
 }
 
-// 16 bytes per lane: lane l writes LDS bytes lds + 16 l .. + 15.
+// 16 bytes per lane: lane l writes LDS bytes lds + 16 l .. + 15.  soff must be
+// wave-uniform (it is made an SGPR here).
 __device__ __forceinline__ void dma_b128(v4s r, const void* lds, int voff, int soff) {
   asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
-               :: "v"(voff), "s"(r), "s"(soff), "{m0}"(lds_addr(lds)) : "memory");
+               :: "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff)), "{m0}"(lds_addr(lds)) : "memory");
 }
 
 // 4 bytes per lane: lane l writes LDS bytes lds + 4 l .. + 3.
 __device__ __forceinline__ void dma_b32(v4s r, const void* lds, int voff, int soff) {
   asm volatile("buffer_load_dword %0, %1, %2 offen lds"
-               :: "v"(voff), "s"(r), "s"(soff), "{m0}"(lds_addr(lds)) : "memory");
+               :: "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff)), "{m0}"(lds_addr(lds)) : "memory");
 }
 
 // s_waitcnt vmcnt(n), also a compiler barrier for memory accesses (the
