@@ -230,9 +230,13 @@ def bench_float(args, dev):
     ops = 2.0 * nb * 1024 * case.N
     if args.op == "sddmm":
         from void_amd import _runtime
+        from void_amd.format import build_bsr_layout
         G = torch.randn(case.M, case.N, device=dev)
         rows, cols = vt.block_rows.to(torch.int32), vt.block_cols.to(torch.int32)
-        run = lambda: _runtime.sddmm_tiles(G, B, rows, cols, (case.M, case.K), torch.float32)
+        # The backward's own path: tiles grouped by block-row (void_sddmm_rows_f32).
+        lay = build_bsr_layout(rows, cols, vt.block_grid[0], vt.block_grid[1], dev)
+        lay.row_groups()
+        run = lambda: _runtime.sddmm_tiles(G, B, rows, cols, (case.M, case.K), torch.float32, layout=lay)
         nbytes = nb * (4096 + 8) + 4 * case.M * case.N + 4 * case.K * case.N
     else:
         out = torch.empty(case.M, case.N, device=dev)
@@ -289,7 +293,7 @@ def bench_float(args, dev):
         cpu = {"value": round(ops / med / 1e12, 4), "unit": "TFLOP/s", "cores": len(os.sched_getaffinity(0)),
                "kind": "port", "ms": round(med * 1e3, 3),
                "sample": f"full {args.config} problem in fp32, torch CPU tile bmm + index_add, median of {len(times) - 1} reps"}
-    what = "SDDMM backward of A (void_sddmm_f32)" if args.op == "sddmm" else "BSpMM (void_spmm)"
+    what = "SDDMM backward of A (void_sddmm_rows_f32)" if args.op == "sddmm" else "BSpMM (void_spmm)"
     line = {"metric": f"FP32 {what} effective TFLOP/s, {case.name} in fp32", "value": round(tflops, 3),
             "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(cold, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,

@@ -233,6 +233,18 @@ int void_sddmm_f32(const float* grad_c, int64_t ldg, const float* b, int64_t ldb
                    const int32_t* block_cols, int32_t n_blocks, int32_t M, int32_t N, int32_t K, void* grad_tiles,
                    int32_t out_dtype, hipStream_t stream);
 
+/* The same gradient with the tiles grouped by block-row, as the SpMM's BSR
+ * order gives them: groups[3 g .. 3 g + 2] = (block row, first BSR position,
+ * tile count <= 8) for n_groups groups, col_idx[k] the block column of BSR
+ * position k, and the gradient of position k written to tile
+ * tile_index[k] of grad_tiles (or tile k when tile_index is null).  Tiles of
+ * one group share one read of their grad_c rows.  Same operand rules as
+ * void_sddmm_f32; also replaces void_spmm_backward_a_kernel
+ * (void/autograd.py:14-97). */
+int void_sddmm_rows_f32(const float* grad_c, int64_t ldg, const float* b, int64_t ldb, const int32_t* groups,
+                        int32_t n_groups, const int32_t* col_idx, const int64_t* tile_index, int32_t M, int32_t N,
+                        int32_t K, void* grad_tiles, int32_t out_dtype, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,4 +1,5 @@
-"""Backward of the float SpMM: the SDDMM kernel (void_sddmm_f32) against
+"""Backward of the float SpMM: the SDDMM kernels (void_sddmm_f32 and the
+row-grouped void_sddmm_rows_f32) against
 float64 products of the same operands, and the autograd wrappers
 (VOIDSpMM, SparseLinear) against float64 dense gradients.  Bound: recursive
 fp32 summation, (n-1) 2^-24 sum|x y| with n the reduction length."""
@@ -16,16 +17,24 @@ pytestmark = pytest.mark.gpu
 U = 2.0 ** -24
 
 
-@pytest.mark.parametrize("M,K,N,n,seed", [(1024, 2048, 512, 600, 0), (100, 70, 36, 6, 1), (64, 96, 130, 5, 2)])
-def test_sddmm_tiles(gpu, M, K, N, n, seed):
+@pytest.mark.parametrize("grouped", [False, True])
+@pytest.mark.parametrize("M,K,N,n,seed", [(1024, 2048, 512, 600, 0), (100, 70, 36, 6, 1), (64, 96, 130, 5, 2),
+                                          (256, 4096, 66, 300, 3)])
+def test_sddmm_tiles(gpu, M, K, N, n, seed, grouped):
+    # grouped: void_sddmm_rows_f32 (tiles of a block-row share their grad_c
+    # rows; the last shape has rows of up to 128 tiles, i.e. many groups per
+    # row); otherwise void_sddmm_f32, one tile per workgroup.
+    from void_amd.format import build_bsr_layout
     rng = np.random.default_rng(seed)
     nbr, nbc = -(-M // 32), -(-K // 32)
     flat = rng.choice(nbr * nbc, min(n, nbr * nbc), replace=False)
     rows, cols = (flat // nbc).astype(np.int32), (flat % nbc).astype(np.int32)
     G = rng.standard_normal((M, N)).astype(np.float32)
     B = rng.standard_normal((K, N)).astype(np.float32)
-    got = _runtime.sddmm_tiles(torch.from_numpy(G).to(gpu), torch.from_numpy(B).to(gpu),
-                               torch.from_numpy(rows).to(gpu), torch.from_numpy(cols).to(gpu), (M, K), torch.float32)
+    tr, tc = torch.from_numpy(rows).to(gpu), torch.from_numpy(cols).to(gpu)
+    lay = build_bsr_layout(tr, tc, nbr, nbc, gpu) if grouped else None
+    got = _runtime.sddmm_tiles(torch.from_numpy(G).to(gpu), torch.from_numpy(B).to(gpu), tr, tc, (M, K),
+                               torch.float32, layout=lay)
     Gp = np.zeros((nbr * 32, N)); Gp[:M] = G
     Bp = np.zeros((nbc * 32, N)); Bp[:K] = B
     for t in range(len(rows)):

@@ -263,8 +263,12 @@ def csr_to_tiles(indptr: np.ndarray, indices: np.ndarray, data: np.ndarray, shap
 
 
 def sddmm_tiles(grad_c: torch.Tensor, b: torch.Tensor, block_rows: torch.Tensor, block_cols: torch.Tensor,
-                shape: Tuple[int, int], out_dtype: torch.dtype) -> torch.Tensor:
-    """[n, 32, 32] gradient of the nonzero tiles: grad_c[rows of t] @ b[cols of t]^T (void_sddmm_f32)."""
+                shape: Tuple[int, int], out_dtype: torch.dtype, layout=None) -> torch.Tensor:
+    """[n, 32, 32] gradient of the nonzero tiles: grad_c[rows of t] @ b[cols of t]^T.
+
+    With the tiles' BsrLayout (block-row order and the Morton index of each
+    position), void_sddmm_rows_f32 shares each block-row's grad_c rows among
+    its tiles; without it, void_sddmm_f32 takes the tiles one by one."""
     M, K = shape
     n = int(block_rows.numel())
     N = grad_c.shape[1]
@@ -275,10 +279,17 @@ def sddmm_tiles(grad_c: torch.Tensor, b: torch.Tensor, block_rows: torch.Tensor,
         return out.zero_()
     g = grad_c.to(torch.float32).contiguous()
     bb = b.to(torch.float32).contiguous()
+    stream = torch.cuda.current_stream(g.device).cuda_stream
+    if layout is not None:
+        groups = layout.row_groups()
+        st = _lib.lib().void_sddmm_rows_f32(g.data_ptr(), g.stride(0), bb.data_ptr(), bb.stride(0), groups.data_ptr(),
+                                            int(groups.shape[0]), layout.col_idx.data_ptr(), layout.order.data_ptr(),
+                                            M, N, K, out.data_ptr(), out_code(out_dtype), stream)
+        _lib.check(st, "void_sddmm_rows_f32")
+        return out
     rows = block_rows.to(device=g.device, dtype=torch.int32).contiguous()
     cols = block_cols.to(device=g.device, dtype=torch.int32).contiguous()
     st = _lib.lib().void_sddmm_f32(g.data_ptr(), g.stride(0), bb.data_ptr(), bb.stride(0), rows.data_ptr(),
-                                   cols.data_ptr(), n, M, N, K, out.data_ptr(), out_code(out_dtype),
-                                   torch.cuda.current_stream(g.device).cuda_stream)
+                                   cols.data_ptr(), n, M, N, K, out.data_ptr(), out_code(out_dtype), stream)
     _lib.check(st, "void_sddmm_f32")
     return out

@@ -69,7 +69,8 @@ class VOIDSpMMFunction(Function):
                      ctx.a_tile_size[::-1], ctx.a_n_blocks)
             grad_b = float_spmm(at, grad_output.contiguous()).to(b.dtype)
         if ctx.needs_input_grad[0]:
-            grad_a = _runtime.sddmm_tiles(grad_output, b, rows, cols, (M, K), a_values.dtype)
+            grad_a = _runtime.sddmm_tiles(grad_output, b, rows, cols, (M, K), a_values.dtype,
+                                          layout=_layout(rows, cols, (M, K)) if rows.is_cuda else None)
         return grad_a, None, None, None, None, None, grad_b
 
 

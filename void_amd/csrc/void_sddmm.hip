@@ -144,6 +144,135 @@ int go(const float* dC, int64_t ldg, const float* B, int64_t ldb, const int32_t*
   return VOID_OK;
 }
 
+// Row-grouped variant (void_sddmm_rows_f32): the tiles of one block-row
+// share their dC rows, so one workgroup of kGW waves takes up to kGW tiles
+// of a block-row (a group).  Per chunk of 32 columns of N the workgroup
+// stages the group's dC block [32 x 32] once in LDS (double-buffered), and
+// each wave streams its own tile's B rows one chunk ahead in registers and
+// runs the chunk's 16 MFMAs with the A operand read from LDS.  dC is then
+// read once per group instead of once per tile.
+constexpr int kGW = 8;
+constexpr int kXPad = 36;  // floats per staged dC row: lanes i and i + 2 land on other banks
+
+template <int OUT, bool VEC>
+__global__ __launch_bounds__(64 * kGW) void sddmm_rows_kernel(
+    const float* __restrict__ dC, int64_t ldg, const float* __restrict__ B, int64_t ldb,
+    const int32_t* __restrict__ groups, const int32_t* __restrict__ col_idx, const int64_t* __restrict__ tile_index,
+    int32_t M, int32_t N, int32_t K, void* __restrict__ grad) {
+  __shared__ __attribute__((aligned(16))) float xs[2][kT][kXPad];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 31, g = lane >> 5;
+  const int br = groups[3 * blockIdx.x], pos0 = groups[3 * blockIdx.x + 1], cnt = groups[3 * blockIdx.x + 2];
+  const bool has = wave < cnt;
+  const int bc = has ? col_idx[pos0 + wave] : 0;
+  const int64_t out_t = has ? (tile_index ? tile_index[pos0 + wave] : (int64_t)(pos0 + wave)) : 0;
+  const int n_chunks = (N + kT - 1) / kT;
+
+  // dC staging: thread tid moves row tid / 16, columns 2 (tid % 16) .. +1.
+  const int xr = tid >> 4, xc = 2 * (tid & 15);
+  const int grow = br * kT + xr;
+  const bool okx = grow < M;
+  const float* xsrc = dC + (int64_t)(okx ? grow : 0) * ldg;
+  // B rows of this wave's tile: lane (i, g) takes row i, columns 16 g .. +15.
+  const int ry = bc * kT + i;
+  const bool oky = has && ry < K;
+  const float* yrow = B + (int64_t)(oky ? ry : 0) * ldb;
+
+  auto load_x = [&](int ch, float& a, float& b2) {
+    const int n = ch * kT + xc;
+    if constexpr (VEC) {
+      const bool in = n < N;  // N even here, so a pair is wholly in or out
+      const float2 v = *reinterpret_cast<const float2*>(xsrc + (in ? n : 0));
+      a = (in && okx) ? v.x : 0.f;
+      b2 = (in && okx) ? v.y : 0.f;
+    } else {
+      const float v0 = xsrc[n < N ? n : 0], v1 = xsrc[n + 1 < N ? n + 1 : 0];
+      a = (n < N && okx) ? v0 : 0.f;
+      b2 = (n + 1 < N && okx) ? v1 : 0.f;
+    }
+  };
+  auto load_y = [&](int ch, v4f (&y)[4]) {
+    const int nb = ch * kT + 16 * g;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = nb + 4 * q;
+      if constexpr (VEC) {
+        const bool in = n < N;
+        const v4f v = *reinterpret_cast<const v4f*>(yrow + (in ? n : 0));
+        y[q] = (in && oky) ? v : v4f{0.f, 0.f, 0.f, 0.f};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool in = n + e < N;
+          const float v = yrow[in ? n + e : 0];
+          y[q][e] = (in && oky) ? v : 0.f;
+        }
+      }
+    }
+  };
+
+  v16f acc = {};
+  v4f y0[4], y1[4];
+  float xa, xb;
+  load_x(0, xa, xb);
+  load_y(0, y0);
+  xs[0][xr][xc] = xa;
+  xs[0][xr][xc + 1] = xb;
+  __syncthreads();
+  for (int ch = 0; ch < n_chunks; ++ch) {
+    const bool more = ch + 1 < n_chunks;
+    if (more) {
+      load_x(ch + 1, xa, xb);
+      load_y(ch + 1, y1);
+    }
+    if (has) {
+      const float* xrow = &xs[ch & 1][i][16 * g];
+      v4f x[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) x[q] = *reinterpret_cast<const v4f*>(xrow + 4 * q);
+#pragma unroll
+      for (int s2 = 0; s2 < 16; ++s2)
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x[s2 >> 2][s2 & 3], y0[s2 >> 2][s2 & 3], acc, 0, 0, 0);
+    }
+    if (more) {
+      xs[(ch + 1) & 1][xr][xc] = xa;
+      xs[(ch + 1) & 1][xr][xc + 1] = xb;
+    }
+    __syncthreads();  // chunk ch + 1 staged; every wave is done with chunk ch's buffer
+#pragma unroll
+    for (int q = 0; q < 4; ++q) y0[q] = y1[q];
+  }
+  if (!has) return;
+  // Lane (j, g), register r: tile row 8 (r / 4) + 4 g + r % 4, column j.
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = 8 * (r >> 2) + 4 * g + (r & 3);
+    const int64_t off = out_t * (kT * kT) + row * kT + i;
+    const float v = acc[r];
+    if constexpr (OUT == VOID_DT_F32) static_cast<float*>(grad)[off] = v;
+    else if constexpr (OUT == VOID_DT_BF16) static_cast<uint16_t*>(grad)[off] = (uint16_t)bf16_bits(v);
+    else {
+      _Float16 h = (_Float16)v;
+      uint16_t u;
+      __builtin_memcpy(&u, &h, 2);
+      static_cast<uint16_t*>(grad)[off] = u;
+    }
+  }
+}
+
+template <int OUT, bool VEC>
+int go_rows(const float* dC, int64_t ldg, const float* B, int64_t ldb, const int32_t* groups, int32_t n_groups,
+            const int32_t* col_idx, const int64_t* tile_index, int32_t M, int32_t N, int32_t K, void* grad,
+            hipStream_t stream) {
+  hipLaunchKernelGGL((sddmm_rows_kernel<OUT, VEC>), dim3(n_groups), dim3(64 * kGW), 0, stream, dC, ldg, B, ldb,
+                     groups, col_idx, tile_index, M, N, K, grad);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return void_internal_fail(VOID_ERR_HIP, hipGetErrorString(e));
+  return VOID_OK;
+}
+
 }  // namespace
 
 extern "C" int void_sddmm_f32(const float* grad_c, int64_t ldg, const float* b, int64_t ldb,
@@ -168,6 +297,33 @@ extern "C" int void_sddmm_f32(const float* grad_c, int64_t ldg, const float* b, 
     case VOID_DT_F16:
       return vec ? go<VOID_DT_F16, true>(grad_c, ldg, b, ldb, block_rows, block_cols, n_blocks, M, N, K, grad_tiles, stream)
                  : go<VOID_DT_F16, false>(grad_c, ldg, b, ldb, block_rows, block_cols, n_blocks, M, N, K, grad_tiles, stream);
+    default:
+      return void_internal_fail(VOID_ERR_UNSUPPORTED, "gradient tiles are f32, bf16 or f16");
+  }
+}
+
+extern "C" int void_sddmm_rows_f32(const float* grad_c, int64_t ldg, const float* b, int64_t ldb,
+                                   const int32_t* groups, int32_t n_groups, const int32_t* col_idx,
+                                   const int64_t* tile_index, int32_t M, int32_t N, int32_t K, void* grad_tiles,
+                                   int32_t out_dtype, hipStream_t stream) {
+  void_internal_fail(VOID_OK, "");
+  if (n_groups < 0 || M < 0 || N < 0 || K < 0) return void_internal_fail(VOID_ERR_ARG, "negative size");
+  if (n_groups == 0) return VOID_OK;
+  if (!grad_c || !b || !groups || !col_idx || !grad_tiles) return void_internal_fail(VOID_ERR_ARG, "null pointer");
+  if (ldg < N || ldb < N) return void_internal_fail(VOID_ERR_ARG, "leading dimension smaller than N");
+  if (N == 0) return void_internal_fail(VOID_ERR_ARG, "N = 0: the gradient is zero, fill it instead");
+  const bool vec = ((uintptr_t)grad_c % 16 == 0) && ((uintptr_t)b % 16 == 0) && ldg % 4 == 0 && ldb % 4 == 0 &&
+                   N % 4 == 0;
+  switch (out_dtype) {
+    case VOID_DT_F32:
+      return vec ? go_rows<VOID_DT_F32, true>(grad_c, ldg, b, ldb, groups, n_groups, col_idx, tile_index, M, N, K, grad_tiles, stream)
+                 : go_rows<VOID_DT_F32, false>(grad_c, ldg, b, ldb, groups, n_groups, col_idx, tile_index, M, N, K, grad_tiles, stream);
+    case VOID_DT_BF16:
+      return vec ? go_rows<VOID_DT_BF16, true>(grad_c, ldg, b, ldb, groups, n_groups, col_idx, tile_index, M, N, K, grad_tiles, stream)
+                 : go_rows<VOID_DT_BF16, false>(grad_c, ldg, b, ldb, groups, n_groups, col_idx, tile_index, M, N, K, grad_tiles, stream);
+    case VOID_DT_F16:
+      return vec ? go_rows<VOID_DT_F16, true>(grad_c, ldg, b, ldb, groups, n_groups, col_idx, tile_index, M, N, K, grad_tiles, stream)
+                 : go_rows<VOID_DT_F16, false>(grad_c, ldg, b, ldb, groups, n_groups, col_idx, tile_index, M, N, K, grad_tiles, stream);
     default:
       return void_internal_fail(VOID_ERR_UNSUPPORTED, "gradient tiles are f32, bf16 or f16");
   }

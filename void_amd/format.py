@@ -64,6 +64,22 @@ class BsrLayout:
     row_ptr: torch.Tensor   # int32 [n_block_rows + 1] on device
     col_idx: torch.Tensor   # int32 [n_blocks] on device
     row_ptr_host: np.ndarray  # int32 copy on the host, for the planner
+    sddmm_groups: Optional[torch.Tensor] = None  # int32 [n_groups, 3], built on first use
+
+    def row_groups(self) -> torch.Tensor:
+        """(block row, first BSR position, count <= 8) per group of a row's tiles,
+        the work list of void_sddmm_rows_f32."""
+        if self.sddmm_groups is None:
+            rp = self.row_ptr_host.astype(np.int64)
+            counts = np.diff(rp)
+            ng = (counts + 7) // 8
+            rows = np.repeat(np.arange(len(counts)), ng)
+            k = np.arange(int(ng.sum())) - np.repeat(np.cumsum(ng) - ng, ng)
+            start = rp[rows] + 8 * k
+            cnt = np.minimum(8, rp[rows + 1] - start)
+            arr = np.stack([rows, start, cnt], axis=1).astype(np.int32).reshape(-1, 3)
+            self.sddmm_groups = torch.from_numpy(arr).to(self.row_ptr.device)
+        return self.sddmm_groups
 
 
 def build_bsr_layout(block_rows: torch.Tensor, block_cols: torch.Tensor, n_block_rows: int,
