@@ -60,7 +60,7 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-enum Elt { kEltI8 = 0, kEltFp8 = 1 };
+enum Elt { kEltI8 = 0, kEltFp8 = 1, kEltF32 = 2 };
 
 struct Params {
   const uint8_t* tiles;
@@ -880,6 +880,19 @@ struct Accum1<kEltFp8, EPI> {
   }
 };
 
+// fp32 tiles (float SpMM): fp32 accumulation, no per-tile scales.
+template <int EPI>
+struct Accum1<kEltF32, EPI> {
+  static constexpr bool kInt = false;
+  using Reg = v16f;
+  using Part = v16f;
+  // Never called: the fp32 tile product is written out in the ring loop; the
+  // register-staged loop that names these is not used for fp32 tiles.
+  __device__ __forceinline__ static void step(Reg&, const Frag1&, float) {}
+  __device__ __forceinline__ static Part prod(const Frag1&) { return Part{}; }
+  __device__ __forceinline__ static void fold(Reg&, const Part&, float) {}
+};
+
 struct CgBatch {
   v4i a[kCgAPerWave];  // A tiles wave + 4q of the batch, lane (j, g): row j, bytes 16g .. 16g+15
   v4i b[kCgBatch];     // row-major B: slab row 8 wave + lane / 8, bytes 16 (lane % 8) .. +15;
@@ -959,14 +972,20 @@ __device__ __forceinline__ void wait_stages(int ahead) {
 template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? kDmaWavesPerEu : 2, DMA ? kDmaWavesPerEu : 2))) void spmm_cg_kernel(Params p) {
   static_assert(!(DMA && BCOL), "the LDS-DMA ring is for row-major B");
+  static_assert(ELT != kEltF32 || DMA, "fp32 tiles only on the LDS-DMA ring");
   using A = Accum1<ELT, EPI>;
   constexpr bool kInt = A::kInt;
-  constexpr bool kScales = (EPI == VOID_EPI_PER_BLOCK);
+  constexpr bool kF32 = ELT == kEltF32;
+  constexpr bool kScales = (EPI == VOID_EPI_PER_BLOCK) && !kF32;
+  // fp32 tiles: 4 bytes per element, one tile (4 KB of A, a 16 KB B slab) per
+  // stage, so the ring keeps its 40 KB and every wave its 5 loads per stage.
+  constexpr int kEsz = kF32 ? 4 : 1;
+  constexpr int kStageTiles = kF32 ? 1 : kDmaTiles;
 
   // Tile slots: two batches of the register-staged loop, or the LDS-DMA ring.
-  constexpr int kSlots = DMA ? kDmaStages * kDmaTiles : 2 * kCgBatch;
-  __shared__ __attribute__((aligned(16))) v4i a_lds[kSlots][64];
-  __shared__ __attribute__((aligned(16))) uint8_t b_lds[BCOL ? 1 : kSlots][BCOL ? 16 : kSlotBytes];
+  constexpr int kSlots = DMA ? kDmaStages * kStageTiles : 2 * kCgBatch;
+  __shared__ __attribute__((aligned(16))) v4i a_lds[kSlots][64 * kEsz];
+  __shared__ __attribute__((aligned(16))) uint8_t b_lds[BCOL ? 1 : kSlots][BCOL ? 16 : kSlotBytes * kEsz];
   // Split-row arrival flag: the first word of the A area, free once every
   // wave has passed the tile loop (no LDS word is spare: 80 KB keeps the
   // register-staged loop at two workgroups per CU, 40 KB the ring at four).
@@ -1009,7 +1028,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
       voff_b_last = (int)(min(brow, p.K - kb_last * kTile - 1) * p.ldb) + cb;
     }
   }
-  const int b_kstride = BCOL ? kTile : kTile * (int)p.ldb;  // bytes per block column
+  const int b_kstride = BCOL ? kTile : kTile * (int)p.ldb * kEsz;  // bytes per block column
 
   // Epilogue inputs, issued before the tile loads (branch-free: a load under
   // a branch would make the compiler's vmcnt waits conservative).
@@ -1019,7 +1038,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
     const float* bip = p.bias ? p.bias : reinterpret_cast<const float*>(p.row_ptr);
     const int cc = min(col, p.N - 1);
     const float vs = sbp[p.b_scale_vec ? cc : 0];
-    const float vb = bip[p.bias ? cc : 0];
+    const float vb = bip[p.bias && !p.bias_per_row ? cc : 0];  // a per-row bias has M entries
     sb = p.b_scale_vec ? vs : p.b_scale;
     bias = p.bias ? vb : 0.f;
   }
@@ -1115,14 +1134,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
   };
 
   if constexpr (DMA) {
-    v4i(*a_ring)[64] = a_lds;
-    uint8_t(*b_ring)[kSlotBytes] = b_lds;
+    v4i(*a_ring)[64 * kEsz] = a_lds;
+    uint8_t(*b_ring)[kSlotBytes * kEsz] = b_lds;
     const v4s da = sgpr_rsrc(p.tiles), db = sgpr_rsrc(p.b), dcol = sgpr_rsrc(p.col_idx), dsc = sgpr_rsrc(p.a_scale);
     // Each wave's own copy of the item's block columns and scales (one per
     // lane), parked in the B area of the last stage's first slot until the
     // first stage has landed: that slot is first refilled after the barrier
     // of stage 0, when every wave has read its copy back.
-    int* win = reinterpret_cast<int*>(&b_ring[(kDmaStages - 1) * kDmaTiles][wave * 512]);
+    int* win = reinterpret_cast<int*>(&b_ring[(kDmaStages - 1) * kStageTiles][wave * 512]);
     if (nt > 0) {
       const int ci = begin + min(lane, nt - 1);
       dma_b32(dcol, win, ci * 4, 0);
@@ -1135,11 +1154,33 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
     cbd = cbd < p.N ? cbd : 0;  // past N: any valid 16 bytes, never stored
     const int voffd = (int)(brow * p.ldb) + cbd;
     const int voffd_last = (kb_last < 0 || brow < p.K - kb_last * kTile) ? voffd : kOutOfRange;
-    const int ns = (nt + kDmaTiles - 1) / kDmaTiles;
+    // fp32: wave w fills rows 8 w .. 8 w + 7 of the slab (512 bytes each), two
+    // rows per load; lane (row r, 16-byte position q) loads chunk q ^ 8 for
+    // r >= 16, so that the two half waves of a column read use other banks.
+    // A tile rows (128 bytes) take the 8-chunk swizzle q ^ (r & 7).
+    int voffs_f[4] = {0, 0, 0, 0};
+    int voff_af = 0;
+    if constexpr (kF32) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int r = 8 * wave + 2 * k + (lane >> 5);
+        int cb = panel * kPanel * 4 + 16 * ((lane & 31) ^ (((r >> 4) & 1) << 3));
+        cb = cb < p.N * 4 ? cb : 0;  // past N: any valid 16 bytes, never stored
+        const int v = (int)(r * p.ldb * 4) + cb;
+        voffs_f[k] = v;
+      }
+      const int ra_row = 8 * wave + (lane >> 3);
+      voff_af = ra_row * (kTile * 4) + 16 * ((lane & 7) ^ (ra_row & 7));
+    }
+    auto voff_f_last = [&](int k) -> int {
+      const int r = 8 * wave + 2 * k + (lane >> 5);
+      return (kb_last < 0 || r < p.K - kb_last * kTile) ? voffs_f[k] : kOutOfRange;
+    };
+    const int ns = (nt + kStageTiles - 1) / kStageTiles;
     // The first kDmaTiles waves also load one A tile per stage.
     const bool a_wave = wave < kDmaTiles;
     auto stage_col = [&](int s, int u) -> int {
-      const int t = s * kDmaTiles + u;
+      const int t = s * kStageTiles + u;
       int kb;
       if (t < 16) {
         // Selects, not a dynamic vector index (that would go through scratch).
@@ -1153,8 +1194,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
       return __builtin_amdgcn_readfirstlane(kb);
     };
     auto issue_stage = [&](int s) {
-      const int slot0 = (s % kDmaStages) * kDmaTiles;
-      const int base = s * kDmaTiles;
+      const int slot0 = (s % kDmaStages) * kStageTiles;
+      const int base = s * kStageTiles;
+      if constexpr (kF32) {
+        const bool live = base < nt;
+        dma_b128(da, &a_ring[slot0][wave * 64], live ? voff_af : kOutOfRange,
+                 (begin + (live ? base : 0)) * (kTile * kTile * 4));
+        const int kb = stage_col(s, 0);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int vo = live ? (kb == kb_last ? voff_f_last(k) : voffs_f[k]) : kOutOfRange;
+          dma_b128(db, &b_ring[slot0][(8 * wave + 2 * k) * (kPanel * 4)], vo, kb * b_kstride);
+        }
+        return;
+      }
       if (a_wave) {
         const int idx = base + wave;
         const bool live = idx < nt;
@@ -1174,7 +1227,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
     TRACE_POINT(1);
     for (int s = 0; s < ns; ++s) {
       const int ahead = min(ns - 1, s + kDmaStages - 2) - s;  // stages issued after s
-      if (a_wave) wait_stages<1 + kDmaTiles>(ahead);
+      if (kF32) wait_stages<5>(ahead);
+      else if (a_wave) wait_stages<1 + kDmaTiles>(ahead);
       else wait_stages<kDmaTiles>(ahead);
       if (s == 0) {
         // The windows were issued before stage 0, so they have landed too.
@@ -1186,9 +1240,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
       // reading stage s - 1, whose slots the next issue overwrites.
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       if (s + kDmaStages - 1 < ns) issue_stage(s + kDmaStages - 1);
-      const int slot0 = (s % kDmaStages) * kDmaTiles;
-      const int base = s * kDmaTiles;
-      if (base + kDmaTiles <= nt) {
+      const int slot0 = (s % kDmaStages) * kStageTiles;
+      const int base = s * kStageTiles;
+      if constexpr (kF32) {
+        // fp32 tile: lane (i, g) holds A row i, columns 16 g .. +15 and B column
+        // 32 wave + i (of the panel), rows 16 g .. +15; MFMA s takes k pair
+        // (s, 16 + s) from both operands.
+        const uint8_t* as = reinterpret_cast<const uint8_t*>(&a_ring[slot0][0]);
+        const uint8_t* bs = &b_ring[slot0][0];
+        v4f af[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          af[q] = *reinterpret_cast<const v4f*>(as + j * (kTile * 4) + (((4 * g + q) ^ (j & 7)) << 4));
+        const int colp = wave * kTile + j;
+        float bf[16];
+#pragma unroll
+        for (int s2 = 0; s2 < 16; ++s2)
+          bf[s2] = *reinterpret_cast<const float*>(bs + (16 * g + s2) * (kPanel * 4) +
+                                                   (((colp >> 2) ^ (g << 3)) << 4) + (colp & 3) * 4);
+#pragma unroll
+        for (int s2 = 0; s2 < 16; ++s2)
+          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s2 >> 2][s2 & 3], bf[s2], acc, 0, 0, 0);
+      } else if (base + kDmaTiles <= nt) {
         // A full stage: all operand reads first, then four independent
         // products, so that one tile's scaling overlaps the next MFMA.
         Frag1 f[kDmaTiles];
@@ -1348,13 +1421,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
     }
     mul = (re > rb) ? __fdiv_rn(S, (float)(re - rb)) : 0.f;
   } else if constexpr (EPI == VOID_EPI_PER_BLOCK) {
-    mul = sb;
+    mul = kF32 ? 1.f : sb;
   }
 
   constexpr int esz = (OUT == VOID_DT_F32 || OUT == VOID_DT_I32) ? 4 : 2;
   const Rsrc rc = make_rsrc(p.c);
   const int ldc = (int)p.ldc;
   const int voff_c = ((4 * g) * ldc + col) * esz;
+  // Per-row bias (FusedSparseLinear): the bias of output row r.
+  auto row_bias = [&](int r) -> float { return p.bias[min(r, p.M - 1)]; };
   const int row0 = row * kTile;
   const bool full = row0 + kTile <= p.M && cg * kTile + kTile <= p.N;
   // LDS-DMA variant, whole block in range and 16-byte aligned rows: the
@@ -1373,7 +1448,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
         float x;
         if constexpr (EPI == VOID_EPI_ROW_MEAN || EPI == VOID_EPI_PER_BLOCK) x = __fmul_rn((float)acc[r], mul);
         else x = 0.f;
-        if (p.bias) x = __fadd_rn(x, bias);
+        if (p.bias) x = __fadd_rn(x, p.bias_per_row ? row_bias(row0 + rr) : bias);
         x = activate(x, p.activation);
         uint8_t* d = stg + rr * kRowB + j * esz;
         if constexpr (OUT == VOID_DT_F32) *reinterpret_cast<float*>(d) = x;
@@ -1404,7 +1479,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
     if constexpr (EPI == VOID_EPI_ROW_MEAN) x = __fmul_rn((float)acc[r], mul);
     else if constexpr (EPI == VOID_EPI_PER_BLOCK) x = __fmul_rn((float)acc[r], mul);
     else x = 0.f;
-    if (p.bias) x = __fadd_rn(x, bias);
+    if (p.bias) x = __fadd_rn(x, p.bias_per_row ? row_bias(row0 + rr + 4 * g) : bias);
     x = activate(x, p.activation);
     if (full || (row0 + rr + 4 * g < p.M && col < p.N)) {
       if constexpr (OUT == VOID_DT_F32) {
@@ -1724,7 +1799,6 @@ int launch_rg(const Params& p, int grid, hipStream_t stream) {
 // loads (one tile ahead) hide the memory latency.  Partial sums of the four
 // waves meet in LDS, as in spmm_bsr_kernel, and split rows use the same
 // coherent fix-up.
-constexpr int kEltF32 = 2;
 
 struct F32Tile {
   v4f a[4];   // A[j][16g + 4q .. 16g + 4q + 3]
@@ -2010,6 +2084,23 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
 
   if (elt == kEltF32) {
     const bool vec = c_ok && (bu % 16 == 0) && (d->ldb % 4 == 0) && (d->N % 4 == 0);
+    // The column-group LDS-DMA ring for row-major B with 16-byte aligned rows,
+    // items of at most 64 tiles and 31-bit byte offsets; VOID_AMD_KERNEL=f32
+    // keeps the fp32 kernel of its own (the fallback for everything else).
+    const char* fk = getenv("VOID_AMD_KERNEL");
+    const int64_t lim = (int64_t)1 << 31;
+    const bool ring_ok = vec && !d->b_col_major && plan->chunk_tiles <= kCgMaxTiles &&
+                         (int64_t)a->n_blocks * kTile * kTile * 4 < lim &&
+                         (int64_t)((a->K + kTile - 1) / kTile) * kTile * d->ldb * 4 < lim &&
+                         (int64_t)a->M * d->ldc * 4 < lim && !(fk && strcmp(fk, "f32") == 0);
+    if (ring_ok) {
+      switch (d->out_dtype) {
+        case VOID_DT_F32: return launch_cg<kEltF32, VOID_EPI_PER_BLOCK, VOID_DT_F32, false, true>(p, grid, stream);
+        case VOID_DT_BF16: return launch_cg<kEltF32, VOID_EPI_PER_BLOCK, VOID_DT_BF16, false, true>(p, grid, stream);
+        case VOID_DT_F16: return launch_cg<kEltF32, VOID_EPI_PER_BLOCK, VOID_DT_F16, false, true>(p, grid, stream);
+        default: return fail(VOID_ERR_UNSUPPORTED, "float SpMM writes f32, bf16 or f16");
+      }
+    }
     switch (d->out_dtype) {
       case VOID_DT_F32: return vec ? launch_f32<VOID_DT_F32, true>(p, grid, stream) : launch_f32<VOID_DT_F32, false>(p, grid, stream);
       case VOID_DT_BF16: return vec ? launch_f32<VOID_DT_BF16, true>(p, grid, stream) : launch_f32<VOID_DT_BF16, false>(p, grid, stream);
