@@ -19,6 +19,18 @@ pytestmark = pytest.mark.gpu
 U = 2.0 ** -24
 
 
+@pytest.fixture(params=["ring", "f32"])
+def fkernel(request, monkeypatch):
+    """The float tiles' two kernels: the column-group LDS-DMA ring (default
+    for row-major 16-byte aligned B; elsewhere the fallback runs anyway) and
+    the fp32 kernel of its own (VOID_AMD_KERNEL=f32)."""
+    if request.param == "f32":
+        monkeypatch.setenv("VOID_AMD_KERNEL", "f32")
+    else:
+        monkeypatch.delenv("VOID_AMD_KERNEL", raising=False)
+    return request.param
+
+
 def _dense_of(vt):
     return oracle.densify(vt.values.float().cpu().numpy(), vt.block_rows.cpu().numpy(), vt.block_cols.cpu().numpy(),
                           vt.shape).astype(np.float64)
@@ -33,7 +45,7 @@ def _bound(vt, B, extra_terms=0):
 
 @pytest.mark.parametrize("M,K,N,n_tiles,seed", [(4096, 4096, 512, 1638, 0), (1024, 2048, 256, 900, 3),
                                                 (96, 96, 64, 9, 1)])
-def test_float_spmm_fp32(gpu, M, K, N, n_tiles, seed):
+def test_float_spmm_fp32(gpu, fkernel, M, K, N, n_tiles, seed):
     case = cases.uniform_blocks(M, K, N, n_tiles, seed=seed)
     vt = cases.make_void_tensor(case, "cpu").to(gpu)
     B = case.b.astype(np.float32)
@@ -46,7 +58,7 @@ def test_float_spmm_fp32(gpu, M, K, N, n_tiles, seed):
 
 
 @pytest.mark.parametrize("M,K,N", [(333, 555, 64), (100, 70, 36), (64, 96, 130), (1000, 70, 257)])
-def test_float_spmm_ragged(gpu, M, K, N):
+def test_float_spmm_ragged(gpu, fkernel, M, K, N):
     rng = np.random.default_rng(M + K + N)
     dense = np.where(rng.random((M, K)) < 0.1, rng.standard_normal((M, K)), 0).astype(np.float32)
     vt = void_amd.dense_to_void(torch.from_numpy(dense)).to(gpu)
@@ -57,7 +69,7 @@ def test_float_spmm_ragged(gpu, M, K, N):
     assert np.all(np.abs(out.cpu().numpy() - ref) <= bound + 1e-30)
 
 
-def test_float_spmm_split_rows(gpu):
+def test_float_spmm_split_rows(gpu, fkernel):
     # Rows of 100 tiles: the 64-tile items split, exercising the fix-up.
     rng = np.random.default_rng(7)
     rows, cols = [], []
@@ -80,7 +92,7 @@ def test_float_spmm_split_rows(gpu):
 
 
 @pytest.mark.parametrize("act", ["gelu", "relu", "silu"])
-def test_float_activation_bias(gpu, act):
+def test_float_activation_bias(gpu, fkernel, act):
     case = cases.uniform_blocks(512, 1024, 192, 120, seed=11)
     vt = cases.make_void_tensor(case, "cpu").to(gpu)
     B = case.b.astype(np.float32)
@@ -95,7 +107,7 @@ def test_float_activation_bias(gpu, act):
     assert np.all(np.abs(out.cpu().numpy() - ref) <= tol)
 
 
-def test_float_bf16_b_and_output(gpu):
+def test_float_bf16_b_and_output(gpu, fkernel):
     case = cases.uniform_blocks(1024, 1024, 256, 300, seed=5)
     vt = cases.make_void_tensor(case, "cpu").to(gpu)
     Bb = torch.from_numpy(case.b).to(torch.bfloat16)
