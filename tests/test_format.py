@@ -118,3 +118,26 @@ def test_dtype_conversions():
     vt = void_amd.csr_to_void(sp.random(64, 64, density=0.2, format="csr", random_state=4))
     assert vt.half().values.dtype == torch.float16 and vt.bfloat16().dtype == torch.bfloat16
     assert vt.float().values.dtype == torch.float32
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_bsr_layout_row_groups(seed):
+    """Work list of the row-grouped SDDMM: every block-row's tiles in runs of
+    at most 8 consecutive BSR positions, in order, covering each tile once."""
+    rng = np.random.default_rng(seed)
+    n_br, n_bc = 40, 64
+    counts = rng.integers(0, 30, size=n_br)
+    counts[rng.integers(0, n_br, size=5)] = 0  # empty rows
+    rows = np.repeat(np.arange(n_br), counts)
+    cols = np.concatenate([np.sort(rng.choice(n_bc, c, replace=False)) for c in counts])
+    lay = build_bsr_layout(torch.from_numpy(rows.astype(np.int32)), torch.from_numpy(cols.astype(np.int32)),
+                           n_br, n_bc, torch.device("cpu"))
+    got = lay.row_groups().numpy()
+    want = []
+    rp = lay.row_ptr_host
+    for r in range(n_br):
+        for s in range(rp[r], rp[r + 1], 8):
+            want.append((r, s, min(8, rp[r + 1] - s)))
+    assert got.dtype == np.int32 and got.shape == (len(want), 3)
+    assert [tuple(x) for x in got.tolist()] == want
+    assert got[:, 2].sum() == len(rows) and got[:, 2].max() <= 8
