@@ -139,11 +139,10 @@ int void_panel_width(void);
 /* Host-side Stream-K planner.  Replaces compute_stream_k_workload
  * (void/stream_k.py:36-110): every block-row becomes one item, except rows
  * with more than chunk_tiles tiles, which are split into ceil(n/chunk_tiles)
- * near-equal chunks.  Items are ordered longest-first -- when rows were
- * split, that list is dealt round-robin into 8 piles laid end to end, so
- * that the contiguous share of the list each XCD runs is a balanced mix --
- * and empty rows are kept (they produce the zero / activation(bias) rows of
- * C).
+ * near-equal chunks.  Items are ordered longest-first (when rows were
+ * split, the SpMM kernels deal the list round-robin among the XCDs that
+ * share a panel group, so that each XCD runs a balanced mix), and empty
+ * rows are kept (they produce the zero / activation(bias) rows of C).
  * row_ptr (n_block_rows + 1 entries) and col_idx (row_ptr[n_block_rows]
  * entries, or NULL to leave cols[] at -1) are HOST arrays.
  * On VOID_ERR_CAPACITY, *n_items holds the required capacity. */

@@ -43,11 +43,9 @@ def _check_plan(row_ptr, col_idx, chunk):
     items, n_tiles, n_slots = _runtime.plan_rows(row_ptr, chunk, col_idx)
     covered = np.zeros(row_ptr[-1], dtype=np.int32)
     lengths = items[:, 2] - items[:, 1]
-    # longest first; with split rows, dealt round-robin into 8 piles laid end to end
+    # longest first (the kernels deal the list among XCDs themselves)
     expect = np.sort(lengths)[::-1]
-    if np.any(items[:, 3] >= 0):
-        expect = np.concatenate([expect[p::8] for p in range(8)])
-    assert np.array_equal(lengths, expect), "items must be longest first (dealt into 8 piles when rows split)"
+    assert np.array_equal(lengths, expect), "items must be longest first"
     tiles, slots = set(), set()
     for it in items:
         row, b, e, tile, nch, ch, slot = it[:7]

@@ -151,6 +151,20 @@ def test_forced_split_row_mean_and_per_block(gpu, chunk, kernel):
     assert np.all(np.abs(pb.cpu().numpy() - refpb) <= 1e-5 * bound + 1e-30)
 
 
+@pytest.mark.parametrize("N", [64, 200, 384, 512, 600])
+def test_split_dealing_geometries(gpu, N, kernel):
+    """Split rows make the kernels deal the work list among the XCDs that
+    share a panel group (8, 4, 2 or 1 of them for 1, 2, 3-4 and 5+ panels),
+    with item counts that do not divide evenly: every item must still run
+    exactly once."""
+    case = cases.uniform_blocks(1056, 1600, N, 700, seed=11)
+    qd, A, bq, bs = _int8_setup(case, gpu)
+    bt = torch.from_numpy(bq).to(gpu)
+    raw = void_amd.void_spmm_int8(qd, bt, b_scale=torch.from_numpy(bs).to(gpu), epilogue="raw_i32", chunk_tiles=3)
+    torch.cuda.synchronize()
+    assert np.array_equal(raw.cpu().numpy(), oracle.i8_acc(A, bq))
+
+
 def test_determinism_split(gpu):
     case = cases.uniform_blocks(512, 4096, 384, 1200, seed=5)
     qd, A, bq, bs = _int8_setup(case, gpu)

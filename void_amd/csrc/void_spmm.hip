@@ -84,6 +84,8 @@ struct Params {
   int32_t activation;
   int32_t n_items;
   int32_t panel_group;  // panels one XCD's share of the grid covers (see wg_tile)
+  int32_t item_piles;   // XCDs among which one panel group's items are dealt (see wg_map)
+  int32_t xcd_exact;    // grid laid out per XCD (see wg_map)
   int32_t bias_per_row;  // float kernel: bias indexed by output row
 };
 
@@ -91,14 +93,20 @@ struct Params {
 // Realtime stamps are kept in scalar registers and written once at exit, so
 // that nothing is stored before the kernel's loads (a store would stop the
 // compiler from using scalar loads for the read-only inputs).
-#define TRACE_DECL unsigned long long tr0 = 0, tr1 = 0, tr2 = 0, tr3 = 0, tr4 = 0, tr5 = 0, tr6 = 0
+#define TRACE_DECL unsigned long long tr0 = 0, tr1 = 0, tr2 = 0, tr3 = 0, tr4 = 0, tr5 = 0, tr6 = 0, tr7 = 0
 #define TRACE_POINT(k) asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(tr##k))
+#define TRACE_TAG(v)                                                           \
+  do {                                                                         \
+    unsigned x_;                                                               \
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x_));          \
+    tr7 = (unsigned long long)(v) | ((unsigned long long)(x_ & 15) << 8);      \
+  } while (0)
 #define TRACE_FLUSH()                                                              \
   do {                                                                             \
     if (p.trace && threadIdx.x == 0) {                                             \
       unsigned long long* t_ = p.trace + (size_t)blockIdx.x * 8;                   \
       t_[0] = tr0; t_[1] = tr1; t_[2] = tr2; t_[3] = tr3;                          \
-      t_[4] = tr4; t_[5] = tr5; t_[6] = tr6;                                       \
+      t_[4] = tr4; t_[5] = tr5; t_[6] = tr6; t_[7] = tr7;                \
     }                                                                              \
   } while (0)
 #else
@@ -107,6 +115,9 @@ struct Params {
   } while (0)
 #define TRACE_POINT(k) \
   do {                 \
+  } while (0)
+#define TRACE_TAG(v) \
+  do {               \
   } while (0)
 #define TRACE_FLUSH() \
   do {                \
@@ -122,12 +133,36 @@ __device__ __forceinline__ int xcd_remap(int h, int G) {
   return x < rem ? x * (per + 1) + s : rem * (per + 1) + (x - rem) * per + s;
 }
 
+// Position r of the work list dealt round-robin into `piles` piles laid end
+// to end -> index into the longest-first list.  Pile p holds list entries
+// p, p + piles, p + 2 piles, ...; the first n % piles piles have one entry
+// more than the rest.
+__device__ __forceinline__ int undeal(int r, int n, int piles) {
+  if (piles <= 1) return r;
+  const int q = n / piles, rem = n - q * piles;
+  const int big = rem * (q + 1);  // entries in the longer piles
+  int pile, k;
+  if (r < big) {
+    pile = r / (q + 1);
+    k = r - pile * (q + 1);
+  } else {  // q >= 1 here: r < n = big + (piles - rem) q
+    const int r2 = r - big;
+    pile = rem + r2 / q;
+    k = r2 - (pile - rem) * q;
+  }
+  return k * piles + pile;
+}
+
 // Logical id -> (work item, panel).  Panels are taken in groups of
 // panel_group (about n_panels / 8, so that one XCD's range covers one group);
 // within a group the order is item-major.  An XCD then reads the B columns
 // of its group's panels only (they stay in its L2), and the panels of one
 // item run back to back on the same XCD, sharing the item's A tiles.
-__device__ __forceinline__ void wg_tile(int L, int n_items, int n_panels, int pgrp, int& item, int& panel) {
+// item_piles > 1 (the XCDs that share one group): the group's items are
+// dealt so that each of those XCDs runs a balanced, still longest-first
+// share of the list rather than a contiguous slice of it.
+__device__ __forceinline__ void wg_tile(int L, int n_items, int n_panels, int pgrp, int item_piles, int& item,
+                                        int& panel) {
   const int full = n_panels / pgrp;  // groups of exactly pgrp panels
   const int gsize = n_items * pgrp;
   int g = L / gsize;
@@ -138,8 +173,34 @@ __device__ __forceinline__ void wg_tile(int L, int n_items, int n_panels, int pg
     w = n_panels - full * pgrp;
     r = L - full * gsize;
   }
-  item = r / w;
-  panel = g * pgrp + (r - item * w);
+  const int pos = r / w;
+  panel = g * pgrp + (r - pos * w);
+  item = undeal(pos, n_items, item_piles);
+}
+
+// Hardware workgroup id -> (work item, panel); false for the padding
+// workgroups of the exact layout below, which do nothing.
+//
+// Exact layout (xcd_exact, set when rows were split and the panel groups
+// divide the 8 XCDs evenly): XCD x = h % 8 serves group x / item_piles and
+// runs every item_piles-th item of the longest-first list, starting at item
+// x % item_piles, one whole item (its panel_group panels back to back) after
+// another.  The grid is 8 x (that share's workgroups, rounded up), so every
+// XCD's share is a longest-first slice of equal length.
+// Otherwise each XCD runs a contiguous range of logical ids (xcd_remap),
+// mapped by wg_tile.
+__device__ __forceinline__ bool wg_map(const Params& p, int& item, int& panel) {
+  const int h = (int)blockIdx.x;
+  if (p.xcd_exact) {
+    const int x = h & 7, s = h >> 3;
+    const int piles = p.item_piles, pg = p.panel_group;
+    const int k = s / pg;
+    panel = (x / piles) * pg + (s - k * pg);
+    item = k * piles + x % piles;
+    return item < p.n_items;
+  }
+  wg_tile(xcd_remap(h, (int)gridDim.x), p.n_items, p.n_panels, p.panel_group, p.item_piles, item, panel);
+  return true;
 }
 
 // 4x4 byte transpose: r_i holds bytes (B[k+i][n+0..3]); c_n gets (B[k+0..3][n]).
@@ -467,9 +528,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int lane = tid & 63;
   const int j = lane & 31, g = lane >> 5;
 
-  const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
   int item_idx, panel;
-  wg_tile(L, p.n_items, p.n_panels, p.panel_group, item_idx, panel);
+  if (!wg_map(p, item_idx, panel)) return;
   const void_work_item* itp = p.items + item_idx;
   // Block columns of the first batch (tiles wave + 4u, u < 4) through the
   // scalar cache, issued together with the record's fields: a cold scalar
@@ -997,9 +1057,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
   const int lane = tid & 63;
   const int j = lane & 31, g = lane >> 5;
 
-  const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
   int item_idx, panel;
-  wg_tile(L, p.n_items, p.n_panels, p.panel_group, item_idx, panel);
+  if (!wg_map(p, item_idx, panel)) return;
   const void_work_item* itp = p.items + item_idx;
   const v4i* colv = reinterpret_cast<const v4i*>(itp->cols);
   const v4i cq0 = colv[0], cq1 = colv[1], cq2 = colv[2], cq3 = colv[3];
@@ -1009,6 +1068,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
   const int cg = panel * kWaves + wave;
   const int col = cg * kTile + j;  // this lane's output column
   TRACE_POINT(0);
+  TRACE_TAG((unsigned long long)nt | ((unsigned long long)blockIdx.x << 16));
 
   const Rsrc ra = make_rsrc(p.tiles), rbm = make_rsrc(p.b), rcol = make_rsrc(p.col_idx),
              rsc = make_rsrc(p.a_scale);
@@ -1560,7 +1620,7 @@ __global__ __launch_bounds__(kRgThreads) __attribute__((amdgpu_waves_per_eu(2, 2
 
   const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
   int grp, panel;
-  wg_tile(L, p.n_items, p.n_panels, p.panel_group, grp, panel);
+  wg_tile(L, p.n_items, p.n_panels, p.panel_group, p.item_piles, grp, panel);
   const int n_br = (p.M + kTile - 1) / kTile;
   const int row = grp * kRgWaves + wave;
   const bool row_ok = row < n_br;
@@ -1816,9 +1876,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int lane = tid & 63;
   const int j = lane & 31, g = lane >> 5;
 
-  const int L = xcd_remap((int)blockIdx.x, (int)gridDim.x);
   int item_idx, panel;
-  wg_tile(L, p.n_items, p.n_panels, p.panel_group, item_idx, panel);
+  if (!wg_map(p, item_idx, panel)) return;
   const void_work_item* itp = p.items + item_idx;
   const int row = itp->row, begin = itp->begin, end = itp->end, split_tile = itp->tile;
   const int nt = end - begin;
@@ -2059,6 +2118,19 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
   p.activation = d->activation;
   p.n_items = n_items;
   p.panel_group = n_panels >= 16 ? n_panels / 8 : 1;
+  // With split rows (a long-tailed distribution) every XCD that shares a
+  // panel group gets a dealt share of the longest-first list; otherwise the
+  // first of them would take all the longest rows.  Without splits the
+  // lengths are close and the plain order measured faster.
+  int64_t grid_exact = 0;
+  {
+    const int n_groups = (n_panels + p.panel_group - 1) / p.panel_group;
+    p.item_piles = n_split_tiles > 0 ? std::max(1, 8 / n_groups) : 1;
+    if (n_split_tiles > 0 && n_panels % p.panel_group == 0 && 8 % n_groups == 0) {
+      p.xcd_exact = 1;
+      grid_exact = 8 * (((int64_t)n_items + p.item_piles - 1) / p.item_piles) * p.panel_group;
+    }
+  }
   p.bias_per_row = d->bias_per_row;
   p.items = items;
   p.trace = g_trace;
@@ -2080,7 +2152,8 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
     layout = kRowLds;
   else
     layout = (c_ok && (bu % 4 == 0) && (d->ldb % 4 == 0)) ? kRowVec : kRowByte;
-  const int grid = (int)grid64;
+  if (grid_exact > 0x7fffffff) return fail(VOID_ERR_ARG, "grid too large");
+  const int grid = p.xcd_exact ? (int)grid_exact : (int)grid64;
 
   if (elt == kEltF32) {
     const bool vec = c_ok && (bu % 16 == 0) && (d->ldb % 4 == 0) && (d->N % 4 == 0);
@@ -2270,26 +2343,12 @@ int void_streamk_plan(const int32_t* row_ptr, const int32_t* col_idx, int32_t n_
     tiles += 1;
     slots += nch;
   }
-  // Longest items first so that the tail of the dispatch is short ones.  When
-  // rows were split (a long-tailed row distribution) the list is then dealt
-  // round-robin into 8 piles laid end to end: the kernels give each XCD a
-  // contiguous range of the work list (for L2 locality), and dealing makes
-  // every such range a balanced mix of long and short items, still longest
-  // first -- otherwise the first XCD receives all of the longest rows
-  // (measured on the power-law config: 84 us undealt, 56 us dealt).  With
-  // no split rows the lengths are close and dealing measured slower (c2:
-  // 12.0 us against 10.2 us), so the plain order is kept.
+  // Longest items first so that the tail of the dispatch is short ones.  The
+  // kernels deal this list among the XCDs that share a panel group when rows
+  // were split (wg_tile), so each XCD's share is a balanced mix.
   std::stable_sort(out.begin(), out.end(), [](const void_work_item& x, const void_work_item& y) {
     return (x.end - x.begin) > (y.end - y.begin);
   });
-  if (tiles > 0) {
-    constexpr size_t kPiles = 8;
-    std::vector<void_work_item> dealt;
-    dealt.reserve(out.size());
-    for (size_t pile = 0; pile < kPiles; ++pile)
-      for (size_t i = pile; i < out.size(); i += kPiles) dealt.push_back(out[i]);
-    out.swap(dealt);
-  }
   *n_items = (int32_t)out.size();
   *n_split_tiles = tiles;
   *n_slots = slots;
