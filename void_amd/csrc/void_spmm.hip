@@ -371,17 +371,39 @@ __device__ __forceinline__ float sigmoid_fast(float t) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t * -1.4426950408889634f));
 }
 
+// fusion.py:38-43: inner = 0.7978845608 (x + 0.044715 x^3) and
+// 0.5 x (1 + tanh(inner)), with tanh(u) = 2 sigmoid(2u) - 1, which is
+// x sigmoid(2 inner) = x / (1 + 2^t), t = x (c0 + c1 x^2),
+// c0 = -2 0.7978845608 log2(e), c1 = 0.044715 c0: three VALU operations
+// and two transcendentals.
+__device__ __forceinline__ float gelu_fast(float x) {
+  constexpr float c0 = -2.0f * 0.7978845608f * 1.4426950408889634f;
+  constexpr float c1 = 0.044715f * c0;
+  const float t = x * __builtin_fmaf(x * x, c1, c0);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
+}
+
 __device__ __forceinline__ float activate(float x, int act) {
   if (act == VOID_ACT_RELU) return fmaxf(x, 0.0f);
-  if (act == VOID_ACT_GELU) {
-    // fusion.py:38-43: inner = 0.7978845608 (x + 0.044715 x^3) and
-    // 0.5 x (1 + tanh(inner)), with tanh(u) = 2 sigmoid(2u) - 1, which is
-    // x sigmoid(2 inner).
-    const float inner = 0.7978845608f * (x + 0.044715f * x * x * x);
-    return x * sigmoid_fast(2.0f * inner);
-  }
+  if (act == VOID_ACT_GELU) return gelu_fast(x);
   if (act == VOID_ACT_SILU) return x * sigmoid_fast(x);
   return x;
+}
+
+// The activation of n values, with the (wave-uniform) choice made once, so
+// the element loop has no branches.
+template <int N>
+__device__ __forceinline__ void activate_all(float (&x)[N], int act) {
+  if (act == VOID_ACT_RELU) {
+#pragma unroll
+    for (int r = 0; r < N; ++r) x[r] = fmaxf(x[r], 0.0f);
+  } else if (act == VOID_ACT_GELU) {
+#pragma unroll
+    for (int r = 0; r < N; ++r) x[r] = gelu_fast(x[r]);
+  } else if (act == VOID_ACT_SILU) {
+#pragma unroll
+    for (int r = 0; r < N; ++r) x[r] = x[r] * sigmoid_fast(x[r]);
+  }
 }
 
 // gfx950's v_cvt_pk_bf16_f32: round to nearest even, NaN stays a (quiet) NaN.
@@ -1502,6 +1524,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
     if (vec) {
       constexpr int kRowB = kTile * esz + 16;  // padded row stride: the two half waves hit other banks
       uint8_t* stg = &b_lds[0][0] + wave * (kTile * kRowB);
+      float xv[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int rr = 8 * (r >> 2) + (r & 3) + 4 * g;
@@ -1509,7 +1532,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
         if constexpr (EPI == VOID_EPI_ROW_MEAN || EPI == VOID_EPI_PER_BLOCK) x = __fmul_rn((float)acc[r], mul);
         else x = 0.f;
         if (p.bias) x = __fadd_rn(x, p.bias_per_row ? row_bias(row0 + rr) : bias);
-        x = activate(x, p.activation);
+        xv[r] = x;
+      }
+      if constexpr (OUT != VOID_DT_I32) activate_all(xv, p.activation);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rr = 8 * (r >> 2) + (r & 3) + 4 * g;
+        const float x = xv[r];
         uint8_t* d = stg + rr * kRowB + j * esz;
         if constexpr (OUT == VOID_DT_F32) *reinterpret_cast<float*>(d) = x;
         else if constexpr (OUT == VOID_DT_I32) *reinterpret_cast<int*>(d) = (int)acc[r];
