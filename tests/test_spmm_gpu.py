@@ -28,11 +28,13 @@ pytestmark = pytest.mark.gpu
 FP8_TOL = 2.0 ** -13
 
 
-@pytest.fixture(params=["cg", "cgd", "bsr", "rg"])
+@pytest.fixture(params=["cg", "cgd", "cgd3", "bsr", "rg"])
 def kernel(request, monkeypatch):
     """Runs a test on each SpMM kernel: the column-group kernel with its
-    LDS-DMA ring (=cgd, the default for row-major B; column-major B runs the
-    register-staged loop), the register-staged column-group loop (=cg), the
+    LDS-DMA ring (=cgd, 4 tiles per stage, the default for row-major B on
+    grids of under four resident rounds; column-major B runs the
+    register-staged loop), the 3-tile ring that larger grids take (=cgd3),
+    the register-staged column-group loop (=cg), the
     general kernel (=bsr) and the row-grouped kernel (=rg, where its
     conditions hold; elsewhere the default dispatch runs)."""
     monkeypatch.setenv("VOID_AMD_KERNEL", request.param)
@@ -130,6 +132,42 @@ def test_c4_powerlaw_streamk_raw(gpu):
     plan = qd.device_bsr().plans
     assert any(p.n_split_tiles > 0 for p in plan.values()), "c4 must exercise split rows"
     assert np.array_equal(out.cpu().numpy(), oracle.i8_acc(A, bq))
+
+
+def test_c5_ffn_full_sampled_rows(gpu, monkeypatch):
+    """Config 5 at full size (14336 x 4096 W at 75 % block sparsity, 2048
+    tokens, GELU in bf16): the default dispatch (a grid of seven resident
+    rounds, which takes the 3-tile ring) must give the same bits as the
+    4-tile ring, and 24 sampled block-rows -- the longest, the shortest, the
+    first, the last and 20 seeded ones -- must match the oracle: int32
+    accumulators bit-exact, the GELU output within bf16 rounding."""
+    case = cases.c5_ffn()
+    qd, A, bq, bs = _int8_setup(case, gpu)
+    bt, st = torch.from_numpy(bq).to(gpu), torch.from_numpy(bs).to(gpu)
+    monkeypatch.delenv("VOID_AMD_KERNEL", raising=False)
+    out = void_amd.void_spmm_gelu(qd, bt, b_scale=st, out_dtype=torch.bfloat16, epilogue="per_block")
+    raw = void_amd.void_spmm_int8(qd, bt, b_scale=st, epilogue="raw_i32")
+    monkeypatch.setenv("VOID_AMD_KERNEL", "cgd")
+    out4 = void_amd.void_spmm_gelu(qd, bt, b_scale=st, out_dtype=torch.bfloat16, epilogue="per_block")
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out4.view(torch.int16))
+
+    lengths = np.diff(A.row_ptr)
+    rng = np.random.default_rng(7)
+    rows = np.unique(np.concatenate([[np.argmax(lengths), np.argmin(lengths), 0, len(lengths) - 1],
+                                     rng.choice(len(lengths), 20, replace=False)]))
+    where = np.full(len(lengths), -1)
+    where[rows] = np.arange(len(rows))
+    keep = where[case.block_rows] >= 0
+    q = void_amd.quantize_void_tensor(cases.make_void_tensor(case, "cpu"))
+    sub = oracle.Bsr(q.values.numpy()[keep], q.scales.numpy()[keep], where[case.block_rows[keep]],
+                     case.block_cols[keep], (len(rows) * 32, case.K))
+    sel = (rows[:, None] * 32 + np.arange(32)[None, :]).reshape(-1)
+    assert np.array_equal(raw.cpu().numpy()[sel], oracle.i8_acc(sub, bq))
+    ref = oracle.gelu_tanh(oracle.i8_per_block(sub, bq, bs))
+    got = out.float().cpu().numpy()[sel]
+    err = np.abs(got - ref)
+    assert np.all(err <= 2.0 ** -8 * np.abs(ref) + 1e-4), err.max()
 
 
 @pytest.mark.parametrize("chunk", [1, 3, 8, 100])

@@ -996,7 +996,14 @@ struct CgBatch {
 constexpr int kDmaTiles = 4;
 constexpr int kDmaStages = 2;
 constexpr int kDmaWavesPerEu = 4;  // workgroups per CU, as LDS (4 x 40 KB) allows
-static_assert(kDmaTiles <= kWaves, "at most one A tile per wave per stage");
+// The deep-grid ring: 3 tiles per stage (30 KB), 5 workgroups per CU.  On
+// grids of several resident rounds the extra waves hide more of each
+// workgroup's start and epilogue (c5: 91 -> 87 us); on one-round grids the
+// shallower stages lose (c3: 11.5 -> 12.6 us).
+constexpr int kDmaTilesDeep = 3;
+constexpr int kDeepGridRounds = 4;  // grids of at least this many 1024-workgroup rounds take it
+__host__ __device__ constexpr int dma_waves_per_eu(int tiles) { return tiles == kDmaTilesDeep ? 5 : kDmaWavesPerEu; }
+static_assert(kDmaTiles <= kWaves && kDmaTilesDeep <= kWaves, "at most one A tile per wave per stage");
 static_assert(kDmaStages >= 2 && kDmaStages <= 4, "stage waits cover up to two stages ahead");
 
 // Cache policy of the staged C stores: nt | sc1 (non-temporal, agent
@@ -1051,8 +1058,8 @@ __device__ __forceinline__ void wait_stages(int ahead) {
   else wait_vm<0>();
 }
 
-template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? kDmaWavesPerEu : 2, DMA ? kDmaWavesPerEu : 2))) void spmm_cg_kernel(Params p) {
+template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false, int RT = kDmaTiles>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? dma_waves_per_eu(RT) : 2, DMA ? dma_waves_per_eu(RT) : 2))) void spmm_cg_kernel(Params p) {
   static_assert(!(DMA && BCOL), "the LDS-DMA ring is for row-major B");
   static_assert(ELT != kEltF32 || DMA, "fp32 tiles only on the LDS-DMA ring");
   using A = Accum1<ELT, EPI>;
@@ -1062,7 +1069,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
   // fp32 tiles: 4 bytes per element, one tile (4 KB of A, a 16 KB B slab) per
   // stage, so the ring keeps its 40 KB and every wave its 5 loads per stage.
   constexpr int kEsz = kF32 ? 4 : 1;
-  constexpr int kStageTiles = kF32 ? 1 : kDmaTiles;
+  constexpr int kStageTiles = kF32 ? 1 : RT;
 
   // Tile slots: two batches of the register-staged loop, or the LDS-DMA ring.
   constexpr int kSlots = DMA ? kDmaStages * kStageTiles : 2 * kCgBatch;
@@ -1259,8 +1266,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
       return (kb_last < 0 || r < p.K - kb_last * kTile) ? voffs_f[k] : kOutOfRange;
     };
     const int ns = (nt + kStageTiles - 1) / kStageTiles;
-    // The first kDmaTiles waves also load one A tile per stage.
-    const bool a_wave = wave < kDmaTiles;
+    // The first RT waves also load one A tile per stage.
+    const bool a_wave = wave < RT;
     auto stage_col = [&](int s, int u) -> int {
       const int t = s * kStageTiles + u;
       int kb;
@@ -1297,7 +1304,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
                  (begin + (live ? idx : 0)) * (kTile * kTile));
       }
 #pragma unroll
-      for (int u = 0; u < kDmaTiles; ++u) {
+      for (int u = 0; u < RT; ++u) {
         const int kb = stage_col(s, u);
         const int vo = base + u < nt ? (kb == kb_last ? voffd_last : voffd) : kOutOfRange;
         dma_b128(db, &b_ring[slot0 + u][wave * (kSlotBytes / kWaves)], vo, kb * b_kstride);
@@ -1310,8 +1317,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
     for (int s = 0; s < ns; ++s) {
       const int ahead = min(ns - 1, s + kDmaStages - 2) - s;  // stages issued after s
       if (kF32) wait_stages<5>(ahead);
-      else if (a_wave) wait_stages<1 + kDmaTiles>(ahead);
-      else wait_stages<kDmaTiles>(ahead);
+      else if (a_wave) wait_stages<1 + RT>(ahead);
+      else wait_stages<RT>(ahead);
       if (s == 0) {
         // The windows were issued before stage 0, so they have landed too.
         colw = win[lane];
@@ -1343,34 +1350,34 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
 #pragma unroll
         for (int s2 = 0; s2 < 16; ++s2)
           acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s2 >> 2][s2 & 3], bf[s2], acc, 0, 0, 0);
-      } else if (base + kDmaTiles <= nt) {
+      } else if (base + RT <= nt) {
         // A full stage: all operand reads first, then four independent
         // products, so that one tile's scaling overlaps the next MFMA.
-        Frag1 f[kDmaTiles];
+        Frag1 f[RT];
 #pragma unroll
-        for (int u = 0; u < kDmaTiles; ++u) {
+        for (int u = 0; u < RT; ++u) {
           f[u].a = a_ring[slot0 + u][lane];
           f[u].b = read_tr(&b_ring[slot0 + u][0], wave, j, g);
         }
         if constexpr (kInt) {
 #pragma unroll
-          for (int u = 0; u < kDmaTiles; ++u) A::step(acc, f[u], 0.f);
+          for (int u = 0; u < RT; ++u) A::step(acc, f[u], 0.f);
         } else {
           // Products two tiles ahead of their scaled adds: the VALU work of
           // tile u runs while the MFMA of tile u + 2 executes.
-          typename A::Part part[kDmaTiles];
+          typename A::Part part[RT];
           part[0] = A::prod(f[0]);
           part[1] = A::prod(f[1]);
 #pragma unroll
-          for (int u = 0; u < kDmaTiles; ++u) {
+          for (int u = 0; u < RT; ++u) {
             __builtin_amdgcn_sched_barrier(0);
-            if (u + 2 < kDmaTiles) part[u + 2] = A::prod(f[u + 2]);
+            if (u + 2 < RT) part[u + 2] = A::prod(f[u + 2]);
             A::fold(acc, part[u], bcast(scw, base + u));
           }
         }
       } else {
 #pragma unroll
-        for (int u = 0; u < kDmaTiles; ++u) {
+        for (int u = 0; u < RT; ++u) {
           if (base + u < nt) {
             Frag1 f;
             f.a = a_ring[slot0 + u][lane];
@@ -1585,9 +1592,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
   TRACE_FLUSH();
 }
 
-template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false>
+template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false, int RT = kDmaTiles>
 int launch_cg(const Params& p, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((spmm_cg_kernel<ELT, EPI, OUT, BCOL, DMA>), dim3(grid), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((spmm_cg_kernel<ELT, EPI, OUT, BCOL, DMA, RT>), dim3(grid), dim3(kThreads), 0, stream, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(VOID_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
   return VOID_OK;
@@ -2224,6 +2231,7 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
   const bool force_bsr = force && strcmp(force, "bsr") == 0;
   const bool force_cg = force && strcmp(force, "cg") == 0;
   const bool force_rg = force && strcmp(force, "rg") == 0;
+  const bool force_deep = force && strcmp(force, "cgd3") == 0;
   const bool offsets_ok = (int64_t)a->n_blocks * kTile * kTile < kLim && b_span < kLim &&
                           (int64_t)a->M * d->ldc * esz < kLim;
 
@@ -2269,12 +2277,17 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
     // Row-major B takes the LDS-DMA ring unless VOID_AMD_KERNEL=cg asks for
     // the register-staged loop.
     const bool dma = !bcol && !force_cg;
+    // Deep grids (several resident rounds) take the 3-tile ring; VOID_AMD_KERNEL=cgd3
+    // forces it.
+    const bool deep = force_deep || (!force && grid >= kDeepGridRounds * 1024);
     auto go = [&](auto elt_c, auto epi_c) -> int {
       constexpr int E = decltype(elt_c)::value, P = decltype(epi_c)::value;
       auto pick = [&](auto out_c) -> int {
         constexpr int O = decltype(out_c)::value;
         if (bcol) return launch_cg<E, P, O, true>(p, grid, stream);
-        return dma ? launch_cg<E, P, O, false, true>(p, grid, stream) : launch_cg<E, P, O, false>(p, grid, stream);
+        if (!dma) return launch_cg<E, P, O, false>(p, grid, stream);
+        return deep ? launch_cg<E, P, O, false, true, kDmaTilesDeep>(p, grid, stream)
+                    : launch_cg<E, P, O, false, true>(p, grid, stream);
       };
       if constexpr (P == VOID_EPI_RAW_I32) {
         return pick(std::integral_constant<int, VOID_DT_I32>{});
