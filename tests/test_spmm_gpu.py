@@ -28,12 +28,14 @@ pytestmark = pytest.mark.gpu
 FP8_TOL = 2.0 ** -13
 
 
-@pytest.fixture(params=["cg", "cgd", "cgd3", "bsr", "rg"])
+@pytest.fixture(params=["cg", "cgd", "cgd3", "cgdk", "bsr", "rg"])
 def kernel(request, monkeypatch):
     """Runs a test on each SpMM kernel: the column-group kernel with its
     LDS-DMA ring (=cgd, 4 tiles per stage, the default for row-major B on
-    grids of under four resident rounds; column-major B runs the
+    grids of one to four resident rounds; column-major B runs the
     register-staged loop), the 3-tile ring that larger grids take (=cgd3),
+    the two-ring 8-wave workgroups that grids of at most 512 workgroups
+    without split rows take (=cgdk; with split rows the default runs),
     the register-staged column-group loop (=cg), the
     general kernel (=bsr) and the row-grouped kernel (=rg, where its
     conditions hold; elsewhere the default dispatch runs)."""

@@ -1002,6 +1002,7 @@ constexpr int kDmaWavesPerEu = 4;  // workgroups per CU, as LDS (4 x 40 KB) allo
 // shallower stages lose (c3: 11.5 -> 12.6 us).
 constexpr int kDmaTilesDeep = 3;
 constexpr int kDeepGridRounds = 4;  // grids of at least this many 1024-workgroup rounds take it
+constexpr int kPairGridMax = 512;   // two-ring (8-wave, 80 KB) workgroups: 2 per CU, one round
 __host__ __device__ constexpr int dma_waves_per_eu(int tiles) { return tiles == kDmaTilesDeep ? 5 : kDmaWavesPerEu; }
 static_assert(kDmaTiles <= kWaves && kDmaTilesDeep <= kWaves, "at most one A tile per wave per stage");
 static_assert(kDmaStages >= 2 && kDmaStages <= 4, "stage waits cover up to two stages ahead");
@@ -1058,9 +1059,11 @@ __device__ __forceinline__ void wait_stages(int ahead) {
   else wait_vm<0>();
 }
 
-template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false, int RT = kDmaTiles>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? dma_waves_per_eu(RT) : 2, DMA ? dma_waves_per_eu(RT) : 2))) void spmm_cg_kernel(Params p) {
+template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false, int RT = kDmaTiles, int KS = 1>
+__global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
+    DMA ? (KS > 1 ? 4 : dma_waves_per_eu(RT)) : 2, DMA ? (KS > 1 ? 4 : dma_waves_per_eu(RT)) : 2))) void spmm_cg_kernel(Params p) {
   static_assert(!(DMA && BCOL), "the LDS-DMA ring is for row-major B");
+  static_assert(KS == 1 || (DMA && ELT != kEltF32 && KS == 2), "the two-ring split is for int8 / fp8 on the LDS-DMA ring");
   static_assert(ELT != kEltF32 || DMA, "fp32 tiles only on the LDS-DMA ring");
   using A = Accum1<ELT, EPI>;
   constexpr bool kInt = A::kInt;
@@ -1072,9 +1075,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
   constexpr int kStageTiles = kF32 ? 1 : RT;
 
   // Tile slots: two batches of the register-staged loop, or the LDS-DMA ring.
+  // KS = 2: two groups of 4 waves, each with its own ring, take alternate
+  // stages of the same item and add their accumulators at the end.
   constexpr int kSlots = DMA ? kDmaStages * kStageTiles : 2 * kCgBatch;
-  __shared__ __attribute__((aligned(16))) v4i a_lds[kSlots][64 * kEsz];
-  __shared__ __attribute__((aligned(16))) uint8_t b_lds[BCOL ? 1 : kSlots][BCOL ? 16 : kSlotBytes * kEsz];
+  __shared__ __attribute__((aligned(16))) v4i a_lds[KS * kSlots][64 * kEsz];
+  __shared__ __attribute__((aligned(16))) uint8_t b_lds[BCOL ? 1 : KS * kSlots][BCOL ? 16 : kSlotBytes * kEsz];
   // Split-row arrival flag: the first word of the A area, free once every
   // wave has passed the tile loop (no LDS word is spare: 80 KB keeps the
   // register-staged loop at two workgroups per CU, 40 KB the ring at four).
@@ -1082,7 +1087,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
 
   TRACE_DECL;
   const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & (kWaves - 1));
+  const int sg = KS > 1 ? __builtin_amdgcn_readfirstlane(tid >> 8) : 0;  // wave group
   const int lane = tid & 63;
   const int j = lane & 31, g = lane >> 5;
 
@@ -1223,8 +1229,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
   };
 
   if constexpr (DMA) {
-    v4i(*a_ring)[64 * kEsz] = a_lds;
-    uint8_t(*b_ring)[kSlotBytes * kEsz] = b_lds;
+    v4i(*a_ring)[64 * kEsz] = a_lds + sg * kSlots;
+    uint8_t(*b_ring)[kSlotBytes * kEsz] = b_lds + sg * kSlots;
     const v4s da = sgpr_rsrc(p.tiles), db = sgpr_rsrc(p.b), dcol = sgpr_rsrc(p.col_idx), dsc = sgpr_rsrc(p.a_scale);
     // Each wave's own copy of the item's block columns and scales (one per
     // lane), parked in the B area of the last stage's first slot until the
@@ -1265,17 +1271,29 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
       const int r = 8 * wave + 2 * k + (lane >> 5);
       return (kb_last < 0 || r < p.K - kb_last * kTile) ? voffs_f[k] : kOutOfRange;
     };
-    const int ns = (nt + kStageTiles - 1) / kStageTiles;
+    // Stages of the item; wave group sg takes global stages sg, sg + KS, ...
+    // (ns of them), and both groups run ns_loop iterations so that they meet
+    // at every barrier.
+    const int ns_all = (nt + kStageTiles - 1) / kStageTiles;
+    const int ns = (ns_all - sg + KS - 1) / KS;
+    const int ns_loop = (ns_all + KS - 1) / KS;
     // The first RT waves also load one A tile per stage.
     const bool a_wave = wave < RT;
+    // Stages issued before the windows land (the prologue, s < kDmaStages - 1,
+    // a constant after unrolling) read their columns from the work item
+    // (tiles below 16); later ones from colw.
+    static_assert((kDmaStages - 1) * KS * kDmaTiles <= 16, "prologue tiles come from the work item");
     auto stage_col = [&](int s, int u) -> int {
-      const int t = s * kStageTiles + u;
+      const int t = (s * KS + sg) * kStageTiles + u;
       int kb;
-      if (t < 16) {
+      if (s < kDmaStages - 1) {
         // Selects, not a dynamic vector index (that would go through scratch).
+        // Element first, then vector, on values (selecting a vector by a
+        // run-time index made the compiler build a table in scratch).
         const int q = t >> 2, e = t & 3;
-        const v4i c = q == 0 ? cq0 : q == 1 ? cq1 : q == 2 ? cq2 : cq3;
-        kb = e == 0 ? c[0] : e == 1 ? c[1] : e == 2 ? c[2] : c[3];
+        auto el = [&](const v4i& c) { return e == 0 ? c[0] : e == 1 ? c[1] : e == 2 ? c[2] : c[3]; };
+        const int k0 = el(cq0), k1 = el(cq1), k2 = el(cq2), k3 = el(cq3);
+        kb = q == 0 ? k0 : q == 1 ? k1 : q == 2 ? k2 : k3;
         kb = kb >= 0 ? kb : max(cq0[0], 0);
       } else {
         kb = __builtin_amdgcn_readlane(colw, min(t, kCgMaxTiles - 1));
@@ -1284,7 +1302,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
     };
     auto issue_stage = [&](int s) {
       const int slot0 = (s % kDmaStages) * kStageTiles;
-      const int base = s * kStageTiles;
+      const int base = (s * KS + sg) * kStageTiles;
       if constexpr (kF32) {
         const bool live = base < nt;
         dma_b128(da, &a_ring[slot0][wave * 64], live ? voff_af : kOutOfRange,
@@ -1314,7 +1332,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
     for (int s = 0; s < kDmaStages - 1; ++s)
       if (s < ns) issue_stage(s);
     TRACE_POINT(1);
-    for (int s = 0; s < ns; ++s) {
+    for (int s = 0; s < ns_loop; ++s) {
+      // Past this group's last stage (s >= ns) ahead is negative: wait for all.
       const int ahead = min(ns - 1, s + kDmaStages - 2) - s;  // stages issued after s
       if (kF32) wait_stages<5>(ahead);
       else if (a_wave) wait_stages<1 + RT>(ahead);
@@ -1329,8 +1348,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
       // reading stage s - 1, whose slots the next issue overwrites.
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       if (s + kDmaStages - 1 < ns) issue_stage(s + kDmaStages - 1);
+      if (KS > 1 && s >= ns) continue;  // the other group's extra stage
       const int slot0 = (s % kDmaStages) * kStageTiles;
-      const int base = s * kStageTiles;
+      const int base = (s * KS + sg) * kStageTiles;
       if constexpr (kF32) {
         // fp32 tile: lane (i, g) holds A row i, columns 16 g .. +15 and B column
         // 32 wave + i (of the panel), rows 16 g .. +15; MFMA s takes k pair
@@ -1389,6 +1409,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     TRACE_POINT(6);
+    if constexpr (KS > 1) {
+      // Group 1 hands its accumulators to group 0 through its own (now idle)
+      // B area, word r of lane l at (wave * 16 + r) * 64 + l, and leaves.
+      int* xb = reinterpret_cast<int*>(&b_lds[kSlots][0]) + wave * 16 * 64;
+      if (sg == 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)  // (__builtin_bit_cast of an element here compiled to element 0 for every r)
+          xb[r * 64 + lane] = kInt ? (int)acc[r] : __float_as_int((float)acc[r]);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (sg == 1) {
+        TRACE_FLUSH();
+        return;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        if constexpr (kInt) acc[r] += xb[r * 64 + lane];
+        else acc[r] += __int_as_float(xb[r * 64 + lane]);
+      }
+    }
   } else if (nt > 0) {
     {
       const int ci = begin + min(lane, nt - 1);
@@ -1592,9 +1632,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DMA ? 
   TRACE_FLUSH();
 }
 
-template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false, int RT = kDmaTiles>
+template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false, int RT = kDmaTiles, int KS = 1>
 int launch_cg(const Params& p, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((spmm_cg_kernel<ELT, EPI, OUT, BCOL, DMA, RT>), dim3(grid), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((spmm_cg_kernel<ELT, EPI, OUT, BCOL, DMA, RT, KS>), dim3(grid), dim3(kThreads * KS), 0, stream, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(VOID_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
   return VOID_OK;
@@ -2232,6 +2272,7 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
   const bool force_cg = force && strcmp(force, "cg") == 0;
   const bool force_rg = force && strcmp(force, "rg") == 0;
   const bool force_deep = force && strcmp(force, "cgd3") == 0;
+  const bool force_pair = force && strcmp(force, "cgdk") == 0;
   const bool offsets_ok = (int64_t)a->n_blocks * kTile * kTile < kLim && b_span < kLim &&
                           (int64_t)a->M * d->ldc * esz < kLim;
 
@@ -2280,14 +2321,20 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
     // Deep grids (several resident rounds) take the 3-tile ring; VOID_AMD_KERNEL=cgd3
     // forces it.
     const bool deep = force_deep || (!force && grid >= kDeepGridRounds * 1024);
+    // Grids that fit in one round at two 8-wave workgroups per CU, with no
+    // split rows, take two rings per workgroup (KS = 2): each wave group
+    // runs half of the item's stages, which halves the longest item's chain
+    // of stage round trips; VOID_AMD_KERNEL=cgdk forces it (where no row is split).
+    const bool pair = !deep && n_split_tiles == 0 && (force_pair || (!force && grid <= kPairGridMax));
     auto go = [&](auto elt_c, auto epi_c) -> int {
       constexpr int E = decltype(elt_c)::value, P = decltype(epi_c)::value;
       auto pick = [&](auto out_c) -> int {
         constexpr int O = decltype(out_c)::value;
         if (bcol) return launch_cg<E, P, O, true>(p, grid, stream);
         if (!dma) return launch_cg<E, P, O, false>(p, grid, stream);
-        return deep ? launch_cg<E, P, O, false, true, kDmaTilesDeep>(p, grid, stream)
-                    : launch_cg<E, P, O, false, true>(p, grid, stream);
+        if (deep) return launch_cg<E, P, O, false, true, kDmaTilesDeep>(p, grid, stream);
+        if (pair) return launch_cg<E, P, O, false, true, kDmaTiles, 2>(p, grid, stream);
+        return launch_cg<E, P, O, false, true>(p, grid, stream);
       };
       if constexpr (P == VOID_EPI_RAW_I32) {
         return pick(std::integral_constant<int, VOID_DT_I32>{});
