@@ -1009,7 +1009,9 @@ static_assert(kDmaStages >= 2 && kDmaStages <= 4, "stage waits cover up to two s
 
 // Cache policy of the staged C stores: nt | sc1 (non-temporal, agent
 // scope).  C is written once and not read by the kernel; on c2 this measured
-// 8.7 us cold / 7.2 us hot against 9.2-9.3 / 8.0 with the default policy.
+// 8.7 us cold / 7.2 us hot against 9.2-9.3 / 8.0 with the default policy
+// (on the later two-ring kernel nt, sc0 | nt, sc0 | sc1 and sc0 | sc1 | nt
+// all measured within noise of it on c2, c3 and c5).
 constexpr int kStoreStream = 2 | 16;
 
 // The loads are inline asm, invisible to the compiler's wait insertion: given
