@@ -136,6 +136,25 @@ def build_problem(cfg: str, dev, epilogue):
     return prob
 
 
+def device_peaks():
+    """The peaks re-derived from this device's reported properties, next to
+    the published figures the roofline fractions divide by: int8 MFMA at
+    4 SIMDs x 2048 ops per clock per CU (v_mfma_i32_32x32x32_i8: 65536 ops
+    in 32 cycles), HBM at the memory clock x bus width x 4 (HBM3E moves 8
+    Gb/s per pin, four transfers per cycle of the 2 GHz clock the device
+    reports).  The reported clocks are the peak ones, so these are ceilings."""
+    from ctypes import byref, c_int32
+    from void_amd import _lib
+    v = [c_int32() for _ in range(4)]
+    if _lib.lib().void_device_info(*(byref(x) for x in v)) != 0:
+        return None
+    cus, sclk, mclk, bus = (x.value for x in v)
+    return {"compute_units": cus, "sclk_mhz": round(sclk / 1e3), "mclk_mhz": round(mclk / 1e3), "bus_bits": bus,
+            "derived_int8_tops": round(cus * 4 * 2048 * sclk * 1e3 / 1e12, 1),
+            "derived_hbm_gbs": round(mclk * 1e3 * bus / 8 * 4 / 1e9, 1),
+            "published_int8_tops": INT8_PEAK_TOPS, "published_hbm_gbs": HBM_PEAK_GBS}
+
+
 def time_gpu(prob, steps: int, warmup: int, flush: bool):
     """Kernel time from HIP-graph replays, so host launch overhead is excluded.
 
@@ -477,7 +496,8 @@ def main():
                   "hot_gbs": round(prob["bytes"] / (hot * 1e-3) / 1e9, 1),
                   "roofline_ms": round(max(t_roof_mem, t_roof_ops) * 1e3, 5),
                   "dense_equiv_tops": round(2.0 * prob["M"] * prob["K"] * prob["N"] / (t_ms * 1e-3) / 1e12, 2),
-                  "wall_s": round(wall, 3)},
+                  "wall_s": round(wall, 3),
+                  "device": device_peaks()},
     }
     if args.config != "c2":
         line["metric"] = f"{prob['kind'].upper()} BSpMM effective TOPS + % roofline, {case.name}"

@@ -136,6 +136,12 @@ const char* void_last_error(void);
 /* Width in columns of the N panel one workgroup computes (128). */
 int void_panel_width(void);
 
+/* Properties of the current device that the roofline peaks are derived from:
+ * compute units, peak engine clock (kHz), peak memory clock (kHz) and memory
+ * bus width (bits).  No counterpart in the reference; used by bench.py to
+ * state the peaks it divides by.  Returns VOID_OK or VOID_ERR_HIP. */
+int void_device_info(int32_t* compute_units, int32_t* sclk_khz, int32_t* mclk_khz, int32_t* bus_bits);
+
 /* Host-side Stream-K planner.  Replaces compute_stream_k_workload
  * (void/stream_k.py:36-110): every block-row becomes one item, except rows
  * with more than chunk_tiles tiles, which are split into ceil(n/chunk_tiles)

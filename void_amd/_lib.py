@@ -95,6 +95,7 @@ SIGNATURES = {
     "void_abi_version": (c_int, []),
     "void_last_error": (c_char_p, []),
     "void_panel_width": (c_int, []),
+    "void_device_info": (c_int, [POINTER(c_int32), POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
     "void_streamk_plan": (c_int, [POINTER(c_int32), POINTER(c_int32), c_int32, c_int32,
                                   POINTER(WorkItem), c_int32, POINTER(c_int32), POINTER(c_int32),
                                   POINTER(c_int32)]),

@@ -2389,6 +2389,23 @@ const char* void_last_error(void) { return g_err; }
 
 int void_panel_width(void) { return kPanel; }
 
+int void_device_info(int32_t* compute_units, int32_t* sclk_khz, int32_t* mclk_khz, int32_t* bus_bits) {
+  g_err[0] = 0;
+  if (!compute_units || !sclk_khz || !mclk_khz || !bus_bits) return fail(VOID_ERR_ARG, "null output pointer");
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  int v[4] = {0, 0, 0, 0};
+  const hipDeviceAttribute_t attrs[4] = {hipDeviceAttributeMultiprocessorCount, hipDeviceAttributeClockRate,
+                                         hipDeviceAttributeMemoryClockRate, hipDeviceAttributeMemoryBusWidth};
+  for (int i = 0; i < 4 && e == hipSuccess; ++i) e = hipDeviceGetAttribute(&v[i], attrs[i], dev);
+  if (e != hipSuccess) return fail(VOID_ERR_HIP, "device attributes: %s", hipGetErrorString(e));
+  *compute_units = v[0];
+  *sclk_khz = v[1];
+  *mclk_khz = v[2];
+  *bus_bits = v[3];
+  return VOID_OK;
+}
+
 #ifdef VOID_TRACE
 // Instrumented builds only: every launch records 8 realtime stamps per
 // workgroup into buf (device memory, >= 8 * grid entries).
