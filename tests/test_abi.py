@@ -207,8 +207,9 @@ def test_analyze_workload_balance():
 def test_chunk_table():
     assert tuning.select_chunk("int8", 1638, 512) == 64                       # c2: no split
     assert tuning.select_chunk("int8", 17960, 256) == 64                      # rows of <= 64 tiles: no split
-    assert tuning.select_chunk("int8", 17960, 256, max_row=512) == 46         # c4: 1.3 x per-slot average
+    assert tuning.select_chunk("int8", 17960, 256, max_row=512) == 64         # c4: 1.3 x per-slot average (91), clamped
     assert tuning.select_chunk("int8", 100, 128, max_row=200) == 32           # clamped to [32, 64]
+    assert tuning.select_chunk("int8", 16000, 128, max_row=200) == 41         # 1.3 x 16000 / 512 slots
     assert tuning.n_panels(512) == 4 and tuning.n_panels(130) == 2
 
 

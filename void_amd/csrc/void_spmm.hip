@@ -1421,14 +1421,18 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
           xb[r * 64 + lane] = kInt ? (int)acc[r] : __float_as_int((float)acc[r]);
       }
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if (sg == 1) {
+      // On a split row group 1 stays, idle, for the split protocol's two
+      // workgroup barriers below and leaves after them.
+      if (sg == 1 && split_tile < 0) {
         TRACE_FLUSH();
         return;
       }
+      if (sg == 0) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        if constexpr (kInt) acc[r] += xb[r * 64 + lane];
-        else acc[r] += __int_as_float(xb[r * 64 + lane]);
+        for (int r = 0; r < 16; ++r) {
+          if constexpr (kInt) acc[r] += xb[r * 64 + lane];
+          else acc[r] += __int_as_float(xb[r * 64 + lane]);
+        }
       }
     }
   } else if (nt > 0) {
@@ -1487,7 +1491,7 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     auto block_of = [&](int c) -> const int* {
       return part + (((size_t)(slot + c) * p.n_panels + panel) * kWaves + wave) * kBlock;
     };
-    {
+    if (sg == 0) {  // (two wave groups: group 0 holds the combined block)
       const Rsrc rp = make_rsrc(block_of(chunk));
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -1505,7 +1509,7 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
       s_last = (old == (unsigned)(nchunks - 1));
     }
     __syncthreads();
-    if (!s_last) {
+    if (!s_last || sg == 1) {
       TRACE_FLUSH();
       return;
     }
@@ -2323,11 +2327,12 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
     // Deep grids (several resident rounds) take the 3-tile ring; VOID_AMD_KERNEL=cgd3
     // forces it.
     const bool deep = force_deep || (!force && grid >= kDeepGridRounds * 1024);
-    // Grids that fit in one round at two 8-wave workgroups per CU, with no
-    // split rows, take two rings per workgroup (KS = 2): each wave group
-    // runs half of the item's stages, which halves the longest item's chain
-    // of stage round trips; VOID_AMD_KERNEL=cgdk forces it (where no row is split).
-    const bool pair = !deep && n_split_tiles == 0 && (force_pair || (!force && grid <= kPairGridMax));
+    // Grids that fit in one round at two 8-wave workgroups per CU, and plans
+    // with split rows (below the deep-grid size), take two rings per
+    // workgroup (KS = 2): each wave group runs half of the item's stages,
+    // which halves the longest item's chain of stage round trips;
+    // VOID_AMD_KERNEL=cgdk forces it.
+    const bool pair = !deep && (force_pair || (!force && (n_split_tiles > 0 || grid <= kPairGridMax)));
     auto go = [&](auto elt_c, auto epi_c) -> int {
       constexpr int E = decltype(elt_c)::value, P = decltype(epi_c)::value;
       auto pick = [&](auto out_c) -> int {

@@ -15,10 +15,12 @@ is fixed by the hardware instead:
   through L2 (coherent 16-byte stores, an atomic, coherent loads):
   - every block-row fits in 64 tiles: chunk 64, nothing is split;
   - some block-row is longer: 1.3 times the average work per resident
-    workgroup slot, clamped to [32, 64].  Measured on the power-law config
-    (Zipf rows up to 512 tiles): chunk 32 36.3 us, 48 35.1 us, 64 36.7 us
-    (event-timed, cold), against 52.8 us for the general kernel at its
-    best chunk (92).
+    workgroup slot, clamped to [32, 64].  Plans with split rows run the
+    two-ring kernel (8-wave workgroups, 2 per CU), so a slot is 1/512 of
+    the chip.  Measured on the power-law config (Zipf rows up to 512 tiles,
+    cold): two-ring kernel at chunk 32 / 46 / 64: 33.4-33.9 / 29.5-30.0 /
+    27.8-28.1 us; the one-ring kernel at 32 / 46 / 64: 30.9-31.0 / 29.4-29.5
+    / 28.5-28.7 us.
 """
 
 from __future__ import annotations
@@ -45,6 +47,10 @@ def resident_workgroups() -> int:
     return GFX950_CUS * WORKGROUPS_PER_CU
 
 
+# Workgroups per CU of the two-ring kernel that plans with split rows run.
+SPLIT_WORKGROUPS_PER_CU = 2
+
+
 def n_panels(N: int) -> int:
     return (N + PANEL_COLUMNS - 1) // PANEL_COLUMNS
 
@@ -55,5 +61,5 @@ def select_chunk(kind: str, n_blocks: int, N: int, max_row: int = 0) -> int:
     cg_max, factor = CHUNK_TABLE[kind]
     if max_row <= cg_max:
         return cg_max
-    per_slot = n_blocks * n_panels(max(N, 1)) / resident_workgroups()
+    per_slot = n_blocks * n_panels(max(N, 1)) / (GFX950_CUS * SPLIT_WORKGROUPS_PER_CU)
     return min(cg_max, max(MIN_SPLIT_CHUNK, int(math.ceil(per_slot * factor))))
