@@ -35,7 +35,7 @@ def kernel(request, monkeypatch):
     grids of one to four resident rounds; column-major B runs the
     register-staged loop), the 3-tile ring that larger grids take (=cgd3),
     the two-ring 8-wave workgroups that grids of at most 512 workgroups
-    without split rows take (=cgdk; with split rows the default runs),
+    and plans with split rows take (=cgdk),
     the register-staged column-group loop (=cg), the
     general kernel (=bsr) and the row-grouped kernel (=rg, where its
     conditions hold; elsewhere the default dispatch runs)."""
