@@ -42,7 +42,7 @@ FP8_PEAK_TFLOPS = 5000.0  # dense MFMA fp8, MI355X
 # FETCH_SIZE and WRITE_SIZE in separate runs of `bench.py --counters`, each
 # scaled by what the same counter reads for a plain 64 MiB copy (FETCH x 1.9993,
 # WRITE x 1.0).  Workloads not listed here report null.
-MEASURED_TRAFFIC = {"c2": 19725950, "c3": 22299452, "c4": 99097999, "c5": 187438356}
+MEASURED_TRAFFIC = {"c2": 19725950, "c3": 22299452, "c4": 91278739, "c5": 187438356}
 
 
 def parse():
