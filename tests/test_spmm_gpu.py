@@ -31,11 +31,10 @@ FP8_TOL = 2.0 ** -13
 @pytest.fixture(params=["cg", "cgd", "cgd3", "cgdk", "bsr", "rg"])
 def kernel(request, monkeypatch):
     """Runs a test on each SpMM kernel: the column-group kernel with its
-    LDS-DMA ring (=cgd, 4 tiles per stage, the default for row-major B on
-    grids of one to four resident rounds; column-major B runs the
-    register-staged loop), the 3-tile ring that larger grids take (=cgd3),
-    the two-ring 8-wave workgroups that grids of at most 512 workgroups
-    and plans with split rows take (=cgdk),
+    LDS-DMA ring of 4 tiles per stage (=cgd; column-major B runs the
+    register-staged loop), the 3-tile ring that unsplit grids beyond 512
+    workgroups take by default (=cgd3), the two-ring 8-wave workgroups that
+    grids of at most 512 workgroups and plans with split rows take (=cgdk),
     the register-staged column-group loop (=cg), the
     general kernel (=bsr) and the row-grouped kernel (=rg, where its
     conditions hold; elsewhere the default dispatch runs)."""

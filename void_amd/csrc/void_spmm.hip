@@ -996,12 +996,13 @@ struct CgBatch {
 constexpr int kDmaTiles = 4;
 constexpr int kDmaStages = 2;
 constexpr int kDmaWavesPerEu = 4;  // workgroups per CU, as LDS (4 x 40 KB) allows
-// The deep-grid ring: 3 tiles per stage (30 KB), 5 workgroups per CU.  On
-// grids of several resident rounds the extra waves hide more of each
-// workgroup's start and epilogue (c5: 91 -> 87 us); on one-round grids the
+// The 3-tile ring: 3 tiles per stage (30 KB), 5 workgroups per CU.  On
+// grids beyond one resident round the extra waves hide more of each
+// workgroup's start and epilogue (c5: 91 -> 87 us; 1024-4096 workgroup
+// uniform grids: 2-5 % over the 4-tile ring); on one-round grids the
 // shallower stages lose (c3: 11.5 -> 12.6 us).
 constexpr int kDmaTilesDeep = 3;
-constexpr int kDeepGridRounds = 4;  // grids of at least this many 1024-workgroup rounds take it
+constexpr int kDeepGridRounds = 4;  // split plans of at least this many 1024-workgroup rounds take it
 constexpr int kPairGridMax = 512;   // two-ring (8-wave, 80 KB) workgroups: 2 per CU, one round
 __host__ __device__ constexpr int dma_waves_per_eu(int tiles) { return tiles == kDmaTilesDeep ? 5 : kDmaWavesPerEu; }
 static_assert(kDmaTiles <= kWaves && kDmaTilesDeep <= kWaves, "at most one A tile per wave per stage");
@@ -2326,13 +2327,18 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
     const bool dma = !bcol && !force_cg;
     // Deep grids (several resident rounds) take the 3-tile ring; VOID_AMD_KERNEL=cgd3
     // forces it.
-    const bool deep = force_deep || (!force && grid >= kDeepGridRounds * 1024);
-    // Grids that fit in one round at two 8-wave workgroups per CU, and plans
-    // with split rows (below the deep-grid size), take two rings per
-    // workgroup (KS = 2): each wave group runs half of the item's stages,
-    // which halves the longest item's chain of stage round trips;
-    // VOID_AMD_KERNEL=cgdk forces it.
-    const bool pair = !deep && (force_pair || (!force && (n_split_tiles > 0 || grid <= kPairGridMax)));
+    // Default ring shapes (measured on c2-c5 and on mid-size uniform grids):
+    //  - grids that fit in one round of two 8-wave workgroups per CU (512),
+    //    and plans with split rows below four resident rounds: two rings per
+    //    workgroup (KS = 2), each wave group running half of the item's
+    //    stages, which halves the longest item's chain of stage round trips;
+    //  - other grids: the 3-tile ring at five workgroups per CU, whose extra
+    //    workgroup hides more of the others' starts and epilogues.
+    // VOID_AMD_KERNEL=cgd / cgd3 / cgdk force the 4-tile ring, the 3-tile
+    // ring or the two-ring workgroups.
+    const bool split_deep = n_split_tiles > 0 && grid >= kDeepGridRounds * 1024;
+    const bool pair = force_pair || (!force && (n_split_tiles > 0 ? !split_deep : grid <= kPairGridMax));
+    const bool deep = !pair && (force_deep || (!force && (n_split_tiles == 0 || split_deep)));
     auto go = [&](auto elt_c, auto epi_c) -> int {
       constexpr int E = decltype(elt_c)::value, P = decltype(epi_c)::value;
       auto pick = [&](auto out_c) -> int {
