@@ -173,6 +173,23 @@ def test_shape_checks():
         void_amd.void_spmm_int8(q, torch.zeros(65, 8, dtype=torch.int8))
 
 
+
+def test_bad_bias_rejected_before_launch():
+    # A bias that is not [N] would let the epilogue read past its end on the
+    # device; both quantised wrappers reject it before touching the GPU.
+    vt = cases.make_void_tensor(cases.uniform_blocks(64, 64, 8, 2, seed=0))
+    q = void_amd.quantize_void_tensor(vt)
+    f8 = void_amd.void_tensor_to_fp8(vt)
+    b8 = torch.zeros(64, 16, dtype=torch.int8)
+    bf8 = torch.zeros(64, 16, dtype=torch.float8_e4m3fn)
+    for bias in (torch.zeros(8), torch.zeros(17), torch.zeros(16, 1)):
+        with pytest.raises(ValueError, match="bias"):
+            void_amd.void_spmm_int8(q, b8, bias=bias)
+        with pytest.raises(ValueError, match="bias"):
+            void_amd.void_spmm_fp8(f8, bf8, bias=bias)
+        with pytest.raises(ValueError, match="bias"):
+            void_amd.void_spmm_gelu(f8, bf8, bias=bias)
+
 # ---------------------------------------------------------------- Stream-K host API
 
 def test_compute_stream_k_workload_balanced():

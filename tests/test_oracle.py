@@ -201,6 +201,27 @@ def test_compute_amax_known_answers():
     assert np.array_equal(scales, (np.array([4.0, 8.0], np.float32) / np.float32(448)).astype(np.float32))
 
 
+def test_quantize_fp8_tensor_known_answers():
+    # Per-tensor amax of the reference's tensor is 8.0 (test_fp8.py:142-143),
+    # so the scale is fl(8 / 448) and x * (1 / scale) is 56 x up to an ulp.
+    t = np.array([[[1.0, 2.0], [3.0, 4.0]], [[5.0, 6.0], [7.0, 8.0]]], np.float32)
+    codes, s = oracle.quantize_fp8_tensor(t)
+    assert s == np.float32(np.float32(8.0) / np.float32(448.0))
+    # Hand-encoded E4M3FN (bias 7): 56 = 1.75 * 2^5 -> 0 1100 110, 112 -> 0 1101 110,
+    # 168 = 1.3125 * 2^7 -> nearest 1.25 * 2^7 = 160 (0 1110 010) or 1.375 * 2^7 = 176
+    # (0 1110 011): 168 is the midpoint, ties to the even mantissa 010; 224 -> 0 1110 110,
+    # 280 = 1.09375 * 2^8 -> 1.125 * 2^8 = 288 (0 1111 001) is nearest; 336 = 1.3125 * 2^8
+    # -> tie between 320 (0 1111 010) and 352 (0 1111 011): even, 0x7A; 392 -> tie between
+    # 384 (0 1111 100) and 416 (0 1111 101): 0x7C; 448 -> 0 1111 110.
+    expect = np.array([[[0x66, 0x6E], [0x72, 0x76]], [[0x79, 0x7A], [0x7C, 0x7E]]], np.uint8)
+    assert np.array_equal(codes, expect), codes
+    # Signs, zero and the all-zero tensor (scale clamped at 1e-12).
+    codes, s = oracle.quantize_fp8_tensor(np.array([-8.0, 0.0, 8.0], np.float32))
+    assert list(codes) == [0xFE, 0x00, 0x7E]
+    codes, s = oracle.quantize_fp8_tensor(np.zeros(4, np.float32))
+    assert s == np.float32(1e-12) and not codes.any()
+
+
 def test_fp8_spmm_equals_dense_float64():
     rng = np.random.default_rng(5)
     dense = np.where(rng.random((64, 128)) < 0.2, rng.standard_normal((64, 128)), 0).astype(np.float32)

@@ -104,24 +104,57 @@ def test_c2_int8_full(gpu, epilogue, kernel):
         assert np.all(err <= 1e-5 * bound + 1e-30), (err / (bound + 1e-30)).max()
 
 
-def test_c3_fp8_full(gpu, kernel):
-    case = cases.c3_fp8()
-    vt = cases.make_void_tensor(case, "cpu")
-    f8 = void_amd.void_tensor_to_fp8(vt)
-    bq, bs = oracle.quantize_fp8_tensor(case.b)
-    bt = torch.from_numpy(bq).to(gpu).view(torch.float8_e4m3fn)
-    out = void_amd.void_spmm_fp8(f8.to(gpu), bt, output_dtype=torch.float32, b_scale=float(bs))
+_C3_CACHE = {}
+
+
+def _c3_fp8_setup():
+    """c3's FP8 A, its E4M3 B and the oracle's product and error scale, computed once."""
+    if not _C3_CACHE:
+        case = cases.c3_fp8()
+        vt = cases.make_void_tensor(case, "cpu")
+        f8 = void_amd.void_tensor_to_fp8(vt)
+        bq, bs = oracle.quantize_fp8_tensor(case.b)
+        A = oracle.Bsr(f8.values_fp8.view(torch.uint8).numpy(), f8.scaling_info.scale.numpy(),
+                       case.block_rows, case.block_cols, (case.M, case.K))
+        Aabs = oracle.Bsr.__new__(oracle.Bsr)
+        Aabs.__dict__.update(A.__dict__)
+        Aabs.tiles = np.ascontiguousarray(A.tiles.view(np.uint8) & 0x7F)
+        _C3_CACHE.update(case=case, f8=f8, bq=bq, bs=bs, ref=oracle.fp8_spmm(A, bq, bs),
+                         bound=oracle.fp8_spmm(Aabs, bq & 0x7F, abs(bs)))
+    return _C3_CACHE
+
+
+# One rounding of the output type (round to nearest even: half an ulp,
+# 2^-9 relative for bf16 and 2^-12 for fp16) on top of the fp32 bound, plus
+# fp16's subnormal spacing.
+_OUT_ROUNDING = {torch.float32: (0.0, 0.0), torch.bfloat16: (2.0 ** -9, 0.0), torch.float16: (2.0 ** -12, 2.0 ** -25)}
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16, torch.float16],
+                         ids=["f32", "bf16", "f16"])
+def test_c3_fp8_full(gpu, kernel, out_dtype):
+    """Config 3 at full size (4096^2 at 80 % block sparsity, E4M3 A and B,
+    N = 512) in each output type: bf16 as the config states, fp16 as the
+    reference's void_spmm_fp8 defaults to (fp8.py:677), and fp32."""
+    d = _c3_fp8_setup()
+    bt = torch.from_numpy(d["bq"]).to(gpu).view(torch.float8_e4m3fn)
+    out = void_amd.void_spmm_fp8(d["f8"].to(gpu), bt, output_dtype=out_dtype, b_scale=float(d["bs"]))
     torch.cuda.synchronize()
-    A = oracle.Bsr(f8.values_fp8.view(torch.uint8).numpy(), f8.scaling_info.scale.numpy(),
-                   case.block_rows, case.block_cols, (case.M, case.K))
-    ref = oracle.fp8_spmm(A, bq, bs)
-    tab = np.abs(oracle.e4m3_table())
-    Aabs = oracle.Bsr.__new__(oracle.Bsr)
-    Aabs.__dict__.update(A.__dict__)
-    Aabs.tiles = np.ascontiguousarray(A.tiles.view(np.uint8) & 0x7F)
-    bound = oracle.fp8_spmm(Aabs, bq & 0x7F, abs(bs))
-    err = np.abs(out.cpu().numpy().astype(np.float64) - ref)
-    assert np.all(err <= FP8_TOL * bound + 1e-30), (err / (bound + 1e-30)).max()
+    assert out.dtype == out_dtype
+    ref, bound = d["ref"], d["bound"]
+    rel, ab = _OUT_ROUNDING[out_dtype]
+    err = np.abs(out.float().cpu().numpy().astype(np.float64) - ref)
+    lim = FP8_TOL * bound * (1 + rel) + rel * np.abs(ref) + ab + 1e-30
+    assert np.all(err <= lim), (err / lim).max()
+
+
+def test_fp8_default_output_is_fp16(gpu):
+    """void_spmm_fp8 without output_dtype writes float16, as the reference."""
+    case = cases.uniform_blocks(256, 512, 96, 40, seed=4)
+    f8 = void_amd.void_tensor_to_fp8(cases.make_void_tensor(case, "cpu")).to(gpu)
+    bq, bs = oracle.quantize_fp8_tensor(case.b)
+    out = void_amd.void_spmm_fp8(f8, torch.from_numpy(bq).to(gpu).view(torch.float8_e4m3fn), b_scale=float(bs))
+    assert out.dtype == torch.float16 and out.shape == (256, 96)
 
 
 def test_c4_powerlaw_streamk_raw(gpu):

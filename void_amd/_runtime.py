@@ -35,18 +35,45 @@ class DevicePlan:
     n_slots: int
     chunk: int
     host_items: np.ndarray       # int32 [n_items, 32] copy, for inspection
-    workspaces: Dict[int, torch.Tensor] = field(default_factory=dict)
+    workspaces: Dict[Tuple[int, int], torch.Tensor] = field(default_factory=dict)
 
-    def workspace(self, N: int, device: torch.device) -> Tuple[Optional[torch.Tensor], int]:
+    def workspace(self, N: int, device: torch.device,
+                  stream: Optional[int] = None) -> Tuple[Optional[torch.Tensor], int]:
+        """The split-row workspace of this plan for N columns on one HIP stream.
+
+        The workspace holds the split rows' arrival counters and partial
+        blocks, so two launches that share one would mix their partials:
+        each stream gets its own (launches on one stream run in order, and
+        every launch leaves the counters at zero).  ``stream`` is the raw
+        stream handle, torch's current stream of ``device`` by default."""
         nbytes = int(_lib.lib().void_workspace_bytes(self.n_split_tiles, self.n_slots, N))
         if nbytes == 0:
             return None, 0
-        ws = self.workspaces.get(nbytes)
+        if stream is None:
+            stream = torch.cuda.current_stream(device).cuda_stream
+        key = (nbytes, int(stream))
+        ws = self.workspaces.get(key)
         if ws is None:
             # Counters must start at zero; every launch leaves them at zero.
-            ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-            self.workspaces[nbytes] = ws
+            # The zeroing runs on the stream that will use the workspace.
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            _zero_on_stream(ws, int(stream), device)
+            self.workspaces[key] = ws
         return ws, nbytes
+
+
+def _zero_on_stream(t: torch.Tensor, stream: int, device: torch.device) -> None:
+    """t.zero_() ordered before later work on the raw HIP stream ``stream``."""
+    cur = torch.cuda.current_stream(device)
+    if cur.cuda_stream == stream:
+        t.zero_()
+        return
+    ext = torch.cuda.ExternalStream(stream, device=device)
+    with torch.cuda.stream(ext):
+        t.zero_()
+    # The allocation came from the current stream's pool; keep it alive for
+    # the external stream as well.
+    t.record_stream(ext)
 
 
 def plan_rows(row_ptr_host: np.ndarray, chunk: int,
@@ -170,7 +197,8 @@ def launch(kind: str, dbsr: DeviceBsr, b: torch.Tensor, *, b_scale: float = 1.0,
     if out.stride(1) != 1 or out.stride(0) < N:
         target = torch.empty(out.shape, dtype=out.dtype, device=out.device)
     plan = dbsr.plan(chunk)
-    ws, ws_bytes = plan.workspace(N, out.device)
+    stream = torch.cuda.current_stream(out.device).cuda_stream
+    ws, ws_bytes = plan.workspace(N, out.device, stream)
     cplan = _lib.Plan(items=plan.items.data_ptr(), n_items=plan.n_items,
                       n_split_tiles=plan.n_split_tiles, n_slots=plan.n_slots, chunk_tiles=plan.chunk)
     dense = _lib.DenseArgs(
@@ -180,7 +208,6 @@ def launch(kind: str, dbsr: DeviceBsr, b: torch.Tensor, *, b_scale: float = 1.0,
         c=target.data_ptr(), ldc=target.stride(0), out_dtype=_OUT_CODES[target.dtype],
         activation=activation)
     desc = dbsr.desc()
-    stream = torch.cuda.current_stream(out.device).cuda_stream
     ws_ptr = ws.data_ptr() if ws is not None else None
     if kind == "int8":
         st = lib.void_spmm_int8(ctypes.byref(desc), ctypes.byref(dense), epilogue, ctypes.byref(cplan),

@@ -203,6 +203,28 @@ __device__ __forceinline__ bool wg_map(const Params& p, int& item, int& panel) {
   return true;
 }
 
+// Split-row fix-up ordering (all three kernels).  The protocol uses no
+// release/acquire fences (at agent scope on gfx950 they write back and
+// invalidate the XCD's whole L2); it is ordered by completion instead:
+//  1. every partial-block access carries agent scope (sc1, the encoding of a
+//     relaxed agent-scope atomic), so each location is coherent across the
+//     8 XCDs;
+//  2. publish_wait: vmcnt(0) returns only when this wave's partial stores
+//     are acknowledged at that scope; the barrier that follows puts every
+//     wave's acknowledgement before thread 0 issues the arrival counter's
+//     RMW;
+//  3. the last arriver issues its partial loads only after the RMW has
+//     returned (its result decides, through LDS and a barrier, whether the
+//     loads run at all), and the hardware issues a wave's memory operations
+//     in order and does not speculate loads, so they observe every
+//     acknowledged store.
+// The hardware waits alone leave the compiler free to move relaxed accesses
+// to other addresses across them; the "memory" clobbers below forbid that.
+__device__ __forceinline__ void publish_wait() {
+  asm volatile("s_waitcnt vmcnt(0) expcnt(0) lgkmcnt(0)" ::: "memory");
+}
+__device__ __forceinline__ void compiler_order() { asm volatile("" ::: "memory"); }
+
 // 4x4 byte transpose: r_i holds bytes (B[k+i][n+0..3]); c_n gets (B[k+0..3][n]).
 __device__ __forceinline__ void transpose4x4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3,
                                              uint32_t& c0, uint32_t& c1, uint32_t& c2,
@@ -754,7 +776,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         __hip_atomic_store(part + off + c, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are acknowledged
+    publish_wait();  // this wave's partial stores are acknowledged
     __syncthreads();
     unsigned* ctr = p.counters + (size_t)tile_id * p.n_panels + panel;
     if (tid == 0) {
@@ -767,6 +789,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       return;
     }
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    compiler_order();  // the partial loads stay below the arrival count
 #pragma unroll
     for (int i = 0; i < kRowsPerWave / 2; ++i) {
       const int rr = wave * kRowsPerWave + 2 * i + g;
@@ -1502,7 +1525,7 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
         __builtin_amdgcn_raw_buffer_store_b128(w, rp, (q * 64 + lane) * 16, 0, kSc1);
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are acknowledged
+    publish_wait();  // this wave's partial stores are acknowledged
     __syncthreads();
     unsigned* ctr = p.counters + (size_t)split_tile * p.n_panels + panel;
     if (tid == 0) {
@@ -1515,6 +1538,7 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
       return;
     }
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    compiler_order();  // the partial loads stay below the arrival count
     // Reduce in chunk order (deterministic), with the loads of four chunks
     // in flight at a time.
     typename A::Reg sum = {};
@@ -2060,7 +2084,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int c = 0; c < 4; ++c)
         __hip_atomic_store(part + off + c, __float_as_int(sum[i][c]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    publish_wait();
     __syncthreads();
     unsigned* ctr = p.counters + (size_t)split_tile * p.n_panels + panel;
     if (tid == 0) {
@@ -2073,6 +2097,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       return;
     }
     if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    compiler_order();  // the partial loads stay below the arrival count
 #pragma unroll
     for (int i = 0; i < kRowsPerWave / 2; ++i) {
       const int rr = wave * kRowsPerWave + 2 * i + g;

@@ -231,11 +231,13 @@ def void_spmm_fp8(a: FP8VOIDTensor, b: torch.Tensor, output_dtype: torch.dtype =
     in fp32 for its TF32 dot, so this path carries B's quantisation error as
     well.  Output dtype float32 / bfloat16 / float16.
     """
-    assert b.dim() == 2
-    assert a.shape[1] == b.shape[0]
-    _runtime.require_gpu(b, "B")
+    if b.dim() != 2 or a.shape[1] != b.shape[0]:
+        raise ValueError(f"B must be [K={a.shape[1]}, N], got {tuple(b.shape)}")
     M, K = a.shape
     N = b.shape[1]
+    if bias is not None and tuple(bias.shape) != (N,):
+        raise ValueError(f"bias must be [{N}], got {tuple(bias.shape)}")
+    _runtime.require_gpu(b, "B")
     if b.dtype != torch.float8_e4m3fn:
         if b.dtype == torch.float8_e5m2:
             raise NotImplementedError("E5M2 B operands are not supported by the gfx950 kernel")
@@ -256,6 +258,8 @@ def void_spmm_fp8(a: FP8VOIDTensor, b: torch.Tensor, output_dtype: torch.dtype =
             out.copy_(apply_activation_torch(out.float() + (bias if bias is not None else 0), activation))
         return out
     _runtime.require_gpu(a.values_fp8, "A")
+    if a.values_fp8.device != b.device:
+        raise ValueError(f"A on {a.values_fp8.device}, B on {b.device}")
     from .fusion import get_activation_code
     if bias is not None:
         bias = bias.to(device=b.device, dtype=torch.float32).contiguous()

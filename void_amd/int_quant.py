@@ -346,6 +346,8 @@ def void_spmm_int8(
     if b.dim() != 2 or b.shape[0] != K:
         raise ValueError(f"B must be [K={K}, N], got {tuple(b.shape)}")
     N = b.shape[1]
+    if bias is not None and tuple(bias.shape) != (N,):
+        raise ValueError(f"bias must be [{N}], got {tuple(bias.shape)}")
     _runtime.require_gpu(b, "B")
     if b.dtype != torch.int8:
         cfg = IntQuantConfig(format=IntFormat.INT8, symmetric=True, scale_mode=ScaleMode.PER_TENSOR)
@@ -377,8 +379,6 @@ def void_spmm_int8(
     dbsr = a.device_bsr()
     chunk = chunk_tiles or tuning.select_chunk("int8", a.n_blocks, N, a.device_bsr().max_row)
     if bias is not None:
-        if bias.shape != (N,):
-            raise ValueError(f"bias must be [{N}]")
         bias = bias.to(device=b.device, dtype=torch.float32).contiguous()
     return _runtime.launch("int8", dbsr, b, b_scale=scalar_scale, b_scale_vec=scale_vec, out=out,
                            epilogue=_lib.EPILOGUES[epilogue], activation=get_activation_code(activation),
