@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define VOID_AMD_ABI_VERSION 2
+#define VOID_AMD_ABI_VERSION 3
 #define VOID_TILE 32
 
 typedef enum void_status {
@@ -176,6 +176,20 @@ int void_spmm_int8(const void_bsr_desc* a, const void_dense_args* d, int32_t epi
  * is always PER_BLOCK: C = s_b * sum_t s_a[t] * (A_t @ B_t). */
 int void_spmm_fp8(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
                   void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* FP8 SpMM with a float B, as the reference computes it when B is not FP8:
+ * C = sum_t s_a[t] * dec(A_t) @ B with B in fp32 (void_spmm_fp8_kernel and
+ * void_spmm_fp8, void/fp8.py:577-742, whose kernel upcasts both operands to
+ * fp32).  a->tiles holds E4M3FN tiles with per-tile (or per-tensor) scales;
+ * d->b is fp32, row-major, with 16-byte aligned rows and N % 4 == 0; the
+ * plan's items have at most 64 tiles.  The E4M3 codes are decoded exactly
+ * to bf16 and each B value is split into bf16 hi + lo on the bf16 MFMA, so
+ * every product is within 2^-16 relative of the exact one (fp32
+ * accumulation).  d->b_scale / b_scale_vec multiply the result (1.0 gives
+ * the reference's semantics); out_dtype f32, bf16 or f16; workspace as for
+ * void_spmm_int8. */
+int void_spmm_fp8_f32b(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
+                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Float SpMM: fp32 tiles times fp32 B on the fp32 MFMA (exact products,
  * fp32 accumulation), then bias, activation and conversion to d->out_dtype

@@ -69,8 +69,10 @@ def lib() -> ctypes.CDLL:
         L.oracle_row_mean.argtypes = [P, i64, P, P, i32, i32, i32, P, P, i64]
         L.oracle_i8_per_block.restype = None
         L.oracle_i8_per_block.argtypes = [P, P, P, P, i32, i32, i32, P, i64, i32, P, P, i64]
-        L.oracle_fp8_spmm.restype = None
+        L.oracle_fp8_spmm.restype = ctypes.c_int
         L.oracle_fp8_spmm.argtypes = [P, P, P, P, i32, i32, i32, P, i64, i32, P, P, i64]
+        L.oracle_fp8_spmm_f32b.restype = ctypes.c_int
+        L.oracle_fp8_spmm_f32b.argtypes = [P, P, P, P, i32, i32, i32, P, i64, i32, P, P, i64]
         L.oracle_e4m3_decode.restype = ctypes.c_double
         L.oracle_e4m3_decode.argtypes = [ctypes.c_uint8]
         L.oracle_gelu_tanh_array.restype = None
@@ -275,8 +277,22 @@ def fp8_spmm(A: Bsr, b_codes: np.ndarray, b_scale) -> np.ndarray:
     N = b.shape[1]
     out = np.zeros((A.M, N), dtype=np.float64)
     tiles = np.ascontiguousarray(A.tiles.view(np.uint8))
-    lib().oracle_fp8_spmm(_p(tiles), _p(A.scales), _p(A.row_ptr), _p(A.col_idx), A.n_block_rows,
-                          A.M, A.K, _p(b), N, N, _p(_sb(b_scale, N)), _p(out), N)
+    if lib().oracle_fp8_spmm(_p(tiles), _p(A.scales), _p(A.row_ptr), _p(A.col_idx), A.n_block_rows,
+                             A.M, A.K, _p(b), N, N, _p(_sb(b_scale, N)), _p(out), N) != 0:
+        raise MemoryError("oracle_fp8_spmm: no memory for the decoded B")
+    return out
+
+
+def fp8_spmm_float_b(A: Bsr, b: np.ndarray, b_scale=1.0) -> np.ndarray:
+    """float64 FP8 SpMM with E4M3 codes for the A tiles and a float32 B, the
+    reference's semantics for a float B (fp8.py:624-671): sum_t s_t dec(A_t) @ B."""
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    N = b.shape[1]
+    out = np.zeros((A.M, N), dtype=np.float64)
+    tiles = np.ascontiguousarray(A.tiles.view(np.uint8))
+    if lib().oracle_fp8_spmm_f32b(_p(tiles), _p(A.scales), _p(A.row_ptr), _p(A.col_idx), A.n_block_rows,
+                                  A.M, A.K, _p(b), N, N, _p(_sb(b_scale, N)), _p(out), N) != 0:
+        raise MemoryError("oracle_fp8_spmm_f32b: no memory for the B copy")
     return out
 
 

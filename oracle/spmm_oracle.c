@@ -14,6 +14,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define TILE 32
@@ -133,12 +134,12 @@ double oracle_e4m3_decode(uint8_t v) {
   return s ? -x : x;
 }
 
-/* FP8 SpMM in double: out[m][n] = s_b[n] * sum_t s_a[t] * sum_k dec(A_t[i][k]) dec(B[kk][n])
- * (fp8.py:624-659 with the fp32 upcast replaced by exact doubles). */
-void oracle_fp8_spmm(const uint8_t* tiles, const float* a_scale, const int32_t* row_ptr,
-                     const int32_t* col_idx, int32_t n_block_rows, int32_t M, int32_t K,
-                     const uint8_t* b, int64_t ldb, int32_t N, const float* s_b, double* out,
-                     int64_t ldout) {
+/* E4M3 SpMM in double with a B given as doubles:
+ * out[m][n] = s_b[n] * sum_t s_a[t] * sum_k dec(A_t[i][k]) b[kk][n]. */
+static void fp8_spmm_dense_b(const uint8_t* tiles, const float* a_scale, const int32_t* row_ptr,
+                             const int32_t* col_idx, int32_t n_block_rows, int32_t M, int32_t K,
+                             const double* b, int64_t ldb, int32_t N, const float* s_b, double* out,
+                             int64_t ldout) {
   double lut[256];
   for (int v = 0; v < 256; ++v) lut[v] = oracle_e4m3_decode((uint8_t)v);
 #pragma omp parallel for schedule(dynamic, 1)
@@ -156,11 +157,11 @@ void oracle_fp8_spmm(const uint8_t* tiles, const float* a_scale, const int32_t* 
         for (int k = 0; k < TILE; ++k) {
           const int64_t kk = (int64_t)col_idx[t] * TILE + k;
           if (kk >= K) break;
-          const uint8_t* brow = b + kk * ldb + n0;
+          const double* brow = b + kk * ldb + n0;
           for (int i = 0; i < TILE; ++i) {
             const double av = lut[tile[i * TILE + k]];
             if (av == 0.0) continue;
-            for (int32_t n = 0; n < nn; ++n) part[i][n] += av * lut[brow[n]];
+            for (int32_t n = 0; n < nn; ++n) part[i][n] += av * brow[n];
           }
         }
         const double s = (double)a_scale[t];
@@ -174,6 +175,40 @@ void oracle_fp8_spmm(const uint8_t* tiles, const float* a_scale, const int32_t* 
       }
     }
   }
+}
+
+/* FP8 SpMM in double: out[m][n] = s_b[n] * sum_t s_a[t] * sum_k dec(A_t[i][k]) dec(B[kk][n])
+ * (fp8.py:624-659 with the fp32 upcast replaced by exact doubles).  Returns 0,
+ * or -1 when the decoded copy of B cannot be allocated. */
+int oracle_fp8_spmm(const uint8_t* tiles, const float* a_scale, const int32_t* row_ptr,
+                    const int32_t* col_idx, int32_t n_block_rows, int32_t M, int32_t K,
+                    const uint8_t* b, int64_t ldb, int32_t N, const float* s_b, double* out,
+                    int64_t ldout) {
+  double lut[256];
+  for (int v = 0; v < 256; ++v) lut[v] = oracle_e4m3_decode((uint8_t)v);
+  double* bd = (double*)malloc(sizeof(double) * ((size_t)K * (size_t)N + 1));
+  if (!bd) return -1;
+  for (int64_t k = 0; k < K; ++k)
+    for (int32_t n = 0; n < N; ++n) bd[k * N + n] = lut[b[k * ldb + n]];
+  fp8_spmm_dense_b(tiles, a_scale, row_ptr, col_idx, n_block_rows, M, K, bd, N, N, s_b, out, ldout);
+  free(bd);
+  return 0;
+}
+
+/* The reference's FP8 SpMM with a float B (fp8.py:624-671: A upcast to fp32
+ * and scaled per tile, B upcast to fp32, fp32 dot), in double:
+ * out[m][n] = s_b[n] * sum_t s_a[t] * sum_k dec(A_t[i][k]) B[kk][n], B fp32. */
+int oracle_fp8_spmm_f32b(const uint8_t* tiles, const float* a_scale, const int32_t* row_ptr,
+                         const int32_t* col_idx, int32_t n_block_rows, int32_t M, int32_t K,
+                         const float* b, int64_t ldb, int32_t N, const float* s_b, double* out,
+                         int64_t ldout) {
+  double* bd = (double*)malloc(sizeof(double) * ((size_t)K * (size_t)N + 1));
+  if (!bd) return -1;
+  for (int64_t k = 0; k < K; ++k)
+    for (int32_t n = 0; n < N; ++n) bd[k * N + n] = (double)b[k * ldb + n];
+  fp8_spmm_dense_b(tiles, a_scale, row_ptr, col_idx, n_block_rows, M, K, bd, N, N, s_b, out, ldout);
+  free(bd);
+  return 0;
 }
 
 /* tanh-form GELU of fusion.py:38-43 in double: 2 sigmoid(2u) - 1 = tanh(u). */

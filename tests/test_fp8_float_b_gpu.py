@@ -1,0 +1,130 @@
+"""GPU parity of the FP8 SpMM with a float B (E4M3 tiles x fp32 B) against
+the oracle's float64 restatement of the reference (fp8.py:624-671).
+
+The kernel decodes the E4M3 codes exactly to bf16 and splits each B value
+into bf16 hi + lo on the bf16 MFMA: every product is within 2^-16 relative
+of the exact one, and the MFMA sums in fp32 with a slightly shortened
+alignment (the same accumulation behaviour as the fp8 MFMA, measured up to
+2e-5 of sum |a b|).  The bar is FP8_TOL = 2^-13 of the product terms'
+magnitude (sum_t s_t |dec A_t| |B| |s_b|), two orders inside the 2e-2 the FP8
+path is specified to, plus one rounding of a 16-bit output type.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import cases
+import oracle
+import void_amd
+
+pytestmark = pytest.mark.gpu
+
+FP8_TOL = 2.0 ** -13
+_OUT_ROUNDING = {torch.float32: (0.0, 0.0), torch.bfloat16: (2.0 ** -8, 0.0), torch.float16: (2.0 ** -11, 2.0 ** -25)}
+
+
+def _setup(case):
+    vt = cases.make_void_tensor(case, "cpu")
+    f8 = void_amd.void_tensor_to_fp8(vt)
+    A = oracle.Bsr(f8.values_fp8.view(torch.uint8).numpy(), f8.scaling_info.scale.numpy(),
+                   case.block_rows, case.block_cols, (case.M, case.K))
+    Aabs = oracle.Bsr.__new__(oracle.Bsr)
+    Aabs.__dict__.update(A.__dict__)
+    Aabs.tiles = np.ascontiguousarray(A.tiles.view(np.uint8) & 0x7F)
+    return f8, A, Aabs
+
+
+def _check(got, ref, bound, out_dtype):
+    rel, ab = _OUT_ROUNDING[out_dtype]
+    err = np.abs(got.astype(np.float64) - ref)
+    lim = FP8_TOL * bound * (1 + rel) + rel * np.abs(ref) + ab + 1e-30
+    assert not np.isnan(got).any()
+    assert np.all(err <= lim), (err / lim).max()
+
+
+_C3 = {}
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32], ids=["f16", "bf16", "f32"])
+def test_c3_fp8_float_b_full(gpu, out_dtype):
+    """Config 3's A (4096^2, 80 % block sparsity, E4M3 per-tile) times its
+    B kept in fp32, the reference's default call (float B, fp16 output)."""
+    if not _C3:
+        case = cases.c3_fp8()
+        f8, A, Aabs = _setup(case)
+        _C3.update(case=case, f8=f8, ref=oracle.fp8_spmm_float_b(A, case.b),
+                   bound=oracle.fp8_spmm_float_b(Aabs, np.abs(case.b)))
+    d = _C3
+    out = void_amd.void_spmm_fp8(d["f8"].to(gpu), torch.from_numpy(d["case"].b).to(gpu), output_dtype=out_dtype)
+    torch.cuda.synchronize()
+    assert out.dtype == out_dtype
+    got = out.float().cpu().numpy()
+    _check(got, d["ref"], d["bound"], out_dtype)
+    # The north star's FP8 tolerance, as a relative error against the
+    # output's scale: far inside.
+    rel = np.abs(got - d["ref"]).max() / np.abs(d["ref"]).max()
+    assert rel < 2e-2
+
+
+@pytest.mark.parametrize("M,K,N", [(333, 555, 64), (100, 70, 37), (64, 200, 130), (32, 32, 1), (1000, 96, 257)])
+def test_fp8_float_b_ragged(gpu, M, K, N):
+    """Ragged M and K (edge tiles, a last B slab crossing K) and N not a
+    multiple of 4 (the wrapper pads B's columns)."""
+    rng = np.random.default_rng(M + K + N)
+    case = cases.uniform_blocks(M, K, N, max(1, (-(-M // 32)) * (-(-K // 32)) // 3), seed=M + N)
+    f8, A, Aabs = _setup(case)
+    out = void_amd.void_spmm_fp8(f8.to(gpu), torch.from_numpy(case.b).to(gpu), output_dtype=torch.float32)
+    _check(out.cpu().numpy(), oracle.fp8_spmm_float_b(A, case.b), oracle.fp8_spmm_float_b(Aabs, np.abs(case.b)),
+           torch.float32)
+
+
+@pytest.mark.parametrize("chunk", [1, 3, 7])
+def test_fp8_float_b_split_rows(gpu, chunk):
+    """Forced Stream-K splits: partial blocks reduced in chunk order."""
+    case = cases.uniform_blocks(1024, 2048, 256, 900, seed=3)
+    f8, A, Aabs = _setup(case)
+    b = torch.from_numpy(case.b).to(gpu)
+    out = void_amd.void_spmm_fp8(f8.to(gpu), b, output_dtype=torch.float32, chunk_tiles=chunk)
+    again = void_amd.void_spmm_fp8(f8.to(gpu), b, output_dtype=torch.float32, chunk_tiles=chunk)
+    assert torch.equal(out.view(torch.int32), again.view(torch.int32))
+    _check(out.cpu().numpy(), oracle.fp8_spmm_float_b(A, case.b), oracle.fp8_spmm_float_b(Aabs, np.abs(case.b)),
+           torch.float32)
+
+
+def test_fp8_float_b_scales_bias_gelu(gpu):
+    """Per-column b_scale, bias and the tanh GELU in bf16, and a bf16 B
+    (upcast exactly, as the reference's .to(tl.float32))."""
+    case = cases.uniform_blocks(256, 512, 192, 60, seed=11)
+    f8, A, Aabs = _setup(case)
+    rng = np.random.default_rng(2)
+    sb = rng.uniform(0.5, 2.0, 192).astype(np.float32)
+    bias = rng.standard_normal(192).astype(np.float32)
+    out = void_amd.void_spmm_gelu(f8.to(gpu), torch.from_numpy(case.b).to(gpu), bias=torch.from_numpy(bias).to(gpu),
+                                  b_scale=torch.from_numpy(sb).to(gpu), out_dtype=torch.bfloat16)
+    pre = oracle.fp8_spmm_float_b(A, case.b, sb) + bias[None, :].astype(np.float64)
+    ref = oracle.gelu_tanh(pre)
+    bound = oracle.fp8_spmm_float_b(Aabs, np.abs(case.b), sb)
+    err = np.abs(out.float().cpu().numpy() - ref)
+    # GELU' is at most 1.13 in magnitude: the pre-activation bound carries over.
+    assert np.all(err <= 1.13 * FP8_TOL * bound + 2.0 ** -8 * np.abs(ref) + 1e-4), err.max()
+    bb = torch.from_numpy(case.b).to(torch.bfloat16)
+    out16 = void_amd.void_spmm_fp8(f8.to(gpu), bb.to(gpu), output_dtype=torch.float32)
+    b16 = bb.float().numpy()
+    _check(out16.cpu().numpy(), oracle.fp8_spmm_float_b(A, b16), oracle.fp8_spmm_float_b(Aabs, np.abs(b16)),
+           torch.float32)
+
+
+def test_fp8_float_b_differs_from_quantised_b(gpu):
+    """A float B is not quantised to E4M3 first: the result tracks the
+    float64 product far closer than the E4M3-B product can (2^-4 relative
+    per B element)."""
+    case = cases.uniform_blocks(512, 1024, 128, 150, seed=21)
+    f8, A, _ = _setup(case)
+    ref = oracle.fp8_spmm_float_b(A, case.b)
+    out = void_amd.void_spmm_fp8(f8.to(gpu), torch.from_numpy(case.b).to(gpu), output_dtype=torch.float32)
+    bq, bs = oracle.quantize_fp8_tensor(case.b)
+    quantised = oracle.fp8_spmm(A, bq, bs)
+    e_gpu = np.abs(out.cpu().numpy() - ref).max()
+    e_q = np.abs(quantised - ref).max()
+    assert e_gpu < e_q / 100, (e_gpu, e_q)

@@ -236,6 +236,29 @@ def test_fp8_spmm_equals_dense_float64():
     assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
 
 
+def test_fp8_spmm_float_b_equals_dense_float64():
+    # The reference's FP8 SpMM with a float B (fp8.py:624-671): E4M3 tiles
+    # decoded and scaled per tile, B kept in fp32.  Against a numpy float64
+    # dense product, on a ragged shape with per-column B scales.
+    rng = np.random.default_rng(8)
+    M, K, N = 70, 100, 37
+    dense = np.where(rng.random((M, K)) < 0.25, rng.standard_normal((M, K)) * 5, 0).astype(np.float32)
+    tiles, br, bc = oracle.csr_tiles(dense)
+    codes, s = oracle.quantize_fp8_blocks(tiles)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    sb = rng.uniform(0.5, 2.0, N).astype(np.float32)
+    A = oracle.Bsr(codes, s, br, bc, (M, K))
+    got = oracle.fp8_spmm_float_b(A, B, sb)
+    tab = oracle.e4m3_table()
+    deq = oracle.densify(tab[codes.astype(np.int64)] * s.astype(np.float64)[:, None, None], br, bc, (M, K))
+    ref = (deq @ B.astype(np.float64)) * sb.astype(np.float64)[None, :]
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
+    # With B holding exactly the values of E4M3 codes it is the FP8 x FP8 product.
+    Bc, bs = oracle.quantize_fp8_tensor(B)
+    assert np.array_equal(oracle.fp8_spmm_float_b(A, tab[Bc.astype(np.int64)].astype(np.float32), 1.0),
+                          oracle.fp8_spmm(A, Bc, 1.0))
+
+
 # ---------------------------------------------------------------- GELU
 
 def test_gelu_tanh_matches_torch():

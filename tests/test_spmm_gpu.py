@@ -124,10 +124,11 @@ def _c3_fp8_setup():
     return _C3_CACHE
 
 
-# One rounding of the output type (round to nearest even: half an ulp,
-# 2^-9 relative for bf16 and 2^-12 for fp16) on top of the fp32 bound, plus
-# fp16's subnormal spacing.
-_OUT_ROUNDING = {torch.float32: (0.0, 0.0), torch.bfloat16: (2.0 ** -9, 0.0), torch.float16: (2.0 ** -12, 2.0 ** -25)}
+# One rounding of the output type on top of the fp32 bound: round to
+# nearest even moves a value by at most the unit roundoff 2^-p relative (p
+# significand bits: 8 for bf16, 11 for fp16), plus half of fp16's subnormal
+# spacing.
+_OUT_ROUNDING = {torch.float32: (0.0, 0.0), torch.bfloat16: (2.0 ** -8, 0.0), torch.float16: (2.0 ** -11, 2.0 ** -25)}
 
 
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16, torch.float16],

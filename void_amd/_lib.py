@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libvoid_amd.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # enum void_epilogue
 EPI_RAW_I32 = 0
@@ -104,6 +104,8 @@ SIGNATURES = {
                                c_void_p, c_size_t, c_void_p]),
     "void_spmm_fp8": (c_int, [POINTER(BsrDesc), POINTER(DenseArgs), POINTER(Plan),
                               c_void_p, c_size_t, c_void_p]),
+    "void_spmm_fp8_f32b": (c_int, [POINTER(BsrDesc), POINTER(DenseArgs), POINTER(Plan),
+                                   c_void_p, c_size_t, c_void_p]),
     "void_spmm_f32": (c_int, [POINTER(BsrDesc), POINTER(DenseArgs), POINTER(Plan),
                               c_void_p, c_size_t, c_void_p]),
     "void_quantize_tiles_i8": (c_int, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p]),

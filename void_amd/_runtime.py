@@ -212,9 +212,14 @@ def launch(kind: str, dbsr: DeviceBsr, b: torch.Tensor, *, b_scale: float = 1.0,
     if kind == "int8":
         st = lib.void_spmm_int8(ctypes.byref(desc), ctypes.byref(dense), epilogue, ctypes.byref(cplan),
                                 ws_ptr, ws_bytes, stream)
-    else:
+    elif kind == "fp8":
         st = lib.void_spmm_fp8(ctypes.byref(desc), ctypes.byref(dense), ctypes.byref(cplan),
                                ws_ptr, ws_bytes, stream)
+    elif kind == "fp8_f32b":
+        st = lib.void_spmm_fp8_f32b(ctypes.byref(desc), ctypes.byref(dense), ctypes.byref(cplan),
+                                    ws_ptr, ws_bytes, stream)
+    else:
+        raise ValueError(f"unknown SpMM kind {kind!r}")
     _lib.check(st, f"void_spmm_{kind}")
     if target is not out:
         out.copy_(target)

@@ -59,8 +59,12 @@ typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 
-enum Elt { kEltI8 = 0, kEltFp8 = 1, kEltF32 = 2 };
+// Tile element types: int8 and E4M3 tiles times a B of the same type; fp32
+// tiles times fp32 B (float SpMM); E4M3 tiles times fp32 B (kEltFp8F32, the
+// reference's FP8 SpMM with a float B).
+enum Elt { kEltI8 = 0, kEltFp8 = 1, kEltF32 = 2, kEltFp8F32 = 3 };
 
 struct Params {
   const uint8_t* tiles;
@@ -998,6 +1002,47 @@ struct Accum1<kEltF32, EPI> {
   __device__ __forceinline__ static void fold(Reg&, const Part&, float) {}
 };
 
+// E4M3 tiles times fp32 B: fp32 accumulation, per-tile scales applied in the
+// ring loop (which computes this product itself, like the fp32 tiles').
+template <int EPI>
+struct Accum1<kEltFp8F32, EPI> : Accum1<kEltF32, EPI> {};
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+
+// Two floats rounded to bf16 (nearest even, v_cvt_pk_bf16_f32), packed.
+__device__ __forceinline__ uint32_t pack_bf16_rne(float x0, float x1) {
+  const v2bf h = {(__bf16)x0, (__bf16)x1};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// The upper halves of two floats (bf16 by truncation), packed.
+__device__ __forceinline__ uint32_t pack_bf16_trunc(float x0, float x1) {
+  return __builtin_amdgcn_perm(__float_as_uint(x1), __float_as_uint(x0), 0x07060302u);
+}
+
+// Four E4M3FN codes (one dword, code i in byte i) -> four bf16 values in two
+// dwords.  Every E4M3 value (subnormals included; the NaN codes stay NaN) is
+// exact in fp32 and in bf16 (3 mantissa bits, exponents 2^-9 .. 2^8), so the
+// truncating pack is exact.
+__device__ __forceinline__ void e4m3x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  const v2f f01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const v2f f23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  lo = pack_bf16_trunc(f01[0], f01[1]);
+  hi = pack_bf16_trunc(f23[0], f23[1]);
+}
+
+// Split of fp32 x into bf16 hi + lo: hi = x truncated to bf16 (x - hi is then
+// exact in fp32 and below 2^-7 |x|), lo = bf16(x - hi) to nearest, so that
+// |x - hi - lo| <= 2^-16 |x| (short of bf16's normal range, x below about
+// 2^-118, lo loses bits).  Two values per call, packed.
+__device__ __forceinline__ void split_bf16(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+  hi = pack_bf16_trunc(x0, x1);
+  const float r0 = x0 - __uint_as_float(__float_as_uint(x0) & 0xffff0000u);
+  const float r1 = x1 - __uint_as_float(__float_as_uint(x1) & 0xffff0000u);
+  lo = pack_bf16_rne(r0, r1);
+}
+
 struct CgBatch {
   v4i a[kCgAPerWave];  // A tiles wave + 4q of the batch, lane (j, g): row j, bytes 16g .. 16g+15
   v4i b[kCgBatch];     // row-major B: slab row 8 wave + lane / 8, bytes 16 (lane % 8) .. +15;
@@ -1089,23 +1134,26 @@ template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false, int RT = kDmaT
 __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     DMA ? (KS > 1 ? 4 : dma_waves_per_eu(RT)) : 2, DMA ? (KS > 1 ? 4 : dma_waves_per_eu(RT)) : 2))) void spmm_cg_kernel(Params p) {
   static_assert(!(DMA && BCOL), "the LDS-DMA ring is for row-major B");
-  static_assert(KS == 1 || (DMA && ELT != kEltF32 && KS == 2), "the two-ring split is for int8 / fp8 on the LDS-DMA ring");
-  static_assert(ELT != kEltF32 || DMA, "fp32 tiles only on the LDS-DMA ring");
+  static_assert(KS == 1 || (DMA && (ELT == kEltI8 || ELT == kEltFp8) && KS == 2),
+                "the two-ring split is for int8 / fp8 on the LDS-DMA ring");
   using A = Accum1<ELT, EPI>;
   constexpr bool kInt = A::kInt;
-  constexpr bool kF32 = ELT == kEltF32;
+  constexpr bool kF32 = ELT == kEltF32;                     // fp32 A tiles
+  constexpr bool kBF32 = kF32 || ELT == kEltFp8F32;         // fp32 B slabs
+  static_assert(!kBF32 || DMA, "fp32 B only on the LDS-DMA ring");
   constexpr bool kScales = (EPI == VOID_EPI_PER_BLOCK) && !kF32;
-  // fp32 tiles: 4 bytes per element, one tile (4 KB of A, a 16 KB B slab) per
-  // stage, so the ring keeps its 40 KB and every wave its 5 loads per stage.
-  constexpr int kEsz = kF32 ? 4 : 1;
-  constexpr int kStageTiles = kF32 ? 1 : RT;
+  // fp32 B: 4 bytes per element, one tile per stage (a 16 KB B slab, and 4 KB
+  // of A for fp32 tiles or 1 KB for E4M3 ones), so the ring keeps its 40 KB.
+  constexpr int kEsz = kF32 ? 4 : 1;    // A
+  constexpr int kBEsz = kBF32 ? 4 : 1;  // B
+  constexpr int kStageTiles = kBF32 ? 1 : RT;
 
   // Tile slots: two batches of the register-staged loop, or the LDS-DMA ring.
   // KS = 2: two groups of 4 waves, each with its own ring, take alternate
   // stages of the same item and add their accumulators at the end.
   constexpr int kSlots = DMA ? kDmaStages * kStageTiles : 2 * kCgBatch;
   __shared__ __attribute__((aligned(16))) v4i a_lds[KS * kSlots][64 * kEsz];
-  __shared__ __attribute__((aligned(16))) uint8_t b_lds[BCOL ? 1 : KS * kSlots][BCOL ? 16 : kSlotBytes * kEsz];
+  __shared__ __attribute__((aligned(16))) uint8_t b_lds[BCOL ? 1 : KS * kSlots][BCOL ? 16 : kSlotBytes * kBEsz];
   // Split-row arrival flag: the first word of the A area, free once every
   // wave has passed the tile loop (no LDS word is spare: 80 KB keeps the
   // register-staged loop at two workgroups per CU, 40 KB the ring at four).
@@ -1149,7 +1197,7 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
       voff_b_last = (int)(min(brow, p.K - kb_last * kTile - 1) * p.ldb) + cb;
     }
   }
-  const int b_kstride = BCOL ? kTile : kTile * (int)p.ldb * kEsz;  // bytes per block column
+  const int b_kstride = BCOL ? kTile : kTile * (int)p.ldb * kBEsz;  // bytes per block column
 
   // Epilogue inputs, issued before the tile loads (branch-free: a load under
   // a branch would make the compiler's vmcnt waits conservative).
@@ -1256,7 +1304,7 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
 
   if constexpr (DMA) {
     v4i(*a_ring)[64 * kEsz] = a_lds + sg * kSlots;
-    uint8_t(*b_ring)[kSlotBytes * kEsz] = b_lds + sg * kSlots;
+    uint8_t(*b_ring)[kSlotBytes * kBEsz] = b_lds + sg * kSlots;
     const v4s da = sgpr_rsrc(p.tiles), db = sgpr_rsrc(p.b), dcol = sgpr_rsrc(p.col_idx), dsc = sgpr_rsrc(p.a_scale);
     // Each wave's own copy of the item's block columns and scales (one per
     // lane), parked in the B area of the last stage's first slot until the
@@ -1281,7 +1329,7 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     // A tile rows (128 bytes) take the 8-chunk swizzle q ^ (r & 7).
     int voffs_f[4] = {0, 0, 0, 0};
     int voff_af = 0;
-    if constexpr (kF32) {
+    if constexpr (kBF32) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int r = 8 * wave + 2 * k + (lane >> 5);
@@ -1303,8 +1351,9 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     const int ns_all = (nt + kStageTiles - 1) / kStageTiles;
     const int ns = (ns_all - sg + KS - 1) / KS;
     const int ns_loop = (ns_all + KS - 1) / KS;
-    // The first RT waves also load one A tile per stage.
-    const bool a_wave = wave < RT;
+    // The first RT waves also load one A tile per stage (wave 0 the one E4M3
+    // tile of a stage with fp32 B; every wave a quarter of an fp32 tile).
+    const bool a_wave = wave < (kBF32 ? 1 : RT);
     // Stages issued before the windows land (the prologue, s < kDmaStages - 1,
     // a constant after unrolling) read their columns from the work item
     // (tiles below 16); later ones from colw.
@@ -1329,10 +1378,14 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     auto issue_stage = [&](int s) {
       const int slot0 = (s % kDmaStages) * kStageTiles;
       const int base = (s * KS + sg) * kStageTiles;
-      if constexpr (kF32) {
+      if constexpr (kBF32) {
         const bool live = base < nt;
-        dma_b128(da, &a_ring[slot0][wave * 64], live ? voff_af : kOutOfRange,
-                 (begin + (live ? base : 0)) * (kTile * kTile * 4));
+        if constexpr (kF32) {
+          dma_b128(da, &a_ring[slot0][wave * 64], live ? voff_af : kOutOfRange,
+                   (begin + (live ? base : 0)) * (kTile * kTile * 4));
+        } else if (a_wave) {
+          dma_b128(da, &a_ring[slot0][0], live ? voff_a : kOutOfRange, (begin + (live ? base : 0)) * (kTile * kTile));
+        }
         const int kb = stage_col(s, 0);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -1362,7 +1415,10 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
       // Past this group's last stage (s >= ns) ahead is negative: wait for all.
       const int ahead = min(ns - 1, s + kDmaStages - 2) - s;  // stages issued after s
       if (kF32) wait_stages<5>(ahead);
-      else if (a_wave) wait_stages<1 + RT>(ahead);
+      else if (kBF32) {
+        if (a_wave) wait_stages<5>(ahead);
+        else wait_stages<4>(ahead);
+      } else if (a_wave) wait_stages<1 + RT>(ahead);
       else wait_stages<RT>(ahead);
       if (s == 0) {
         // The windows were issued before stage 0, so they have landed too.
@@ -1396,6 +1452,52 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
         for (int s2 = 0; s2 < 16; ++s2)
           acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s2 >> 2][s2 & 3], bf[s2], acc, 0, 0, 0);
+      } else if constexpr (ELT == kEltFp8F32) {
+        // E4M3 tile times fp32 B on the bf16 MFMA: lane (i, g) holds A row i,
+        // k = 16 g .. 16 g + 15 (its 16 codes, decoded exactly to bf16) and B
+        // column 32 wave + i, the same 16 rows, split into bf16 hi + lo.  MFMA
+        // h (h = 0, 1) takes k = 16 g + 8 h .. + 7 from both operands, once
+        // with hi and once with lo: A (hi + lo) is within 2^-16 of A B per
+        // product, and the tile's scale multiplies the fp32 sum.
+        const v4i araw = a_ring[slot0][lane];
+        v4i a8[2];
+        {
+          uint32_t d[8];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) e4m3x4_to_bf16((uint32_t)araw[q], d[2 * q], d[2 * q + 1]);
+          a8[0] = v4i{(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
+          a8[1] = v4i{(int)d[4], (int)d[5], (int)d[6], (int)d[7]};
+        }
+        const uint8_t* bs = &b_ring[slot0][0];
+        const int colp = wave * kTile + j;
+        float bf[16];
+#pragma unroll
+        for (int s2 = 0; s2 < 16; ++s2)
+          bf[s2] = *reinterpret_cast<const float*>(bs + (16 * g + s2) * (kPanel * 4) +
+                                                   (((colp >> 2) ^ (g << 3)) << 4) + (colp & 3) * 4);
+        v4i bh[2], bl[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            uint32_t hi, lo;
+            split_bf16(bf[8 * h + 2 * q], bf[8 * h + 2 * q + 1], hi, lo);
+            bh[h][q] = (int)hi;
+            bl[h][q] = (int)lo;
+          }
+        }
+        v16f part = {};
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          part = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a8[h]), __builtin_bit_cast(v8bf, bh[h]),
+                                                         part, 0, 0, 0);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          part = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a8[h]), __builtin_bit_cast(v8bf, bl[h]),
+                                                         part, 0, 0, 0);
+        const float sc = bcast(scw, base);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = __builtin_fmaf(sc, part[r], acc[r]);
       } else if (base + RT <= nt) {
         // A full stage: all operand reads first, then four independent
         // products, so that one tile's scaling overlaps the next MFMA.
@@ -2194,11 +2296,12 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
     return fail(VOID_ERR_UNSUPPORTED, "RAW_I32 epilogue and I32 output go together");
   if (elt == kEltFp8 && epilogue != VOID_EPI_PER_BLOCK)
     return fail(VOID_ERR_UNSUPPORTED, "fp8 SpMM supports only the per-block epilogue");
-  if (elt == kEltF32 && d->b_col_major) return fail(VOID_ERR_UNSUPPORTED, "float SpMM takes a row-major B");
+  const bool b_f32 = elt == kEltF32 || elt == kEltFp8F32;
+  if (b_f32 && d->b_col_major) return fail(VOID_ERR_UNSUPPORTED, "an fp32 B must be row-major");
   if (d->bias_per_row && elt != kEltF32)
     return fail(VOID_ERR_UNSUPPORTED, "a per-row bias is supported by the float SpMM only");
-  if (elt == kEltF32 && plan->chunk_tiles > 64)
-    return fail(VOID_ERR_ARG, "float SpMM takes work items of at most 64 tiles (chunk_tiles %d)", plan->chunk_tiles);
+  if (b_f32 && plan->chunk_tiles > 64)
+    return fail(VOID_ERR_ARG, "an fp32 B takes work items of at most 64 tiles (chunk_tiles %d)", plan->chunk_tiles);
   if (d->activation < VOID_ACT_NONE || d->activation > VOID_ACT_SILU)
     return fail(VOID_ERR_ARG, "unknown activation %d", d->activation);
 
@@ -2263,6 +2366,23 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
   if (grid_exact > 0x7fffffff) return fail(VOID_ERR_ARG, "grid too large");
   const int grid = p.xcd_exact ? (int)grid_exact : (int)grid64;
 
+  if (elt == kEltFp8F32) {
+    // E4M3 tiles times fp32 B: the LDS-DMA ring only (16-byte aligned rows,
+    // N % 4 == 0, 31-bit byte offsets); the Python wrapper pads other shapes.
+    const int64_t lim = (int64_t)1 << 31;
+    const int esz = (d->out_dtype == VOID_DT_BF16 || d->out_dtype == VOID_DT_F16) ? 2 : 4;
+    if (!(c_ok && (bu % 16 == 0) && (d->ldb % 4 == 0)))
+      return fail(VOID_ERR_UNSUPPORTED, "E4M3 x fp32 SpMM needs 16-byte aligned B and C rows and N %% 4 == 0");
+    if (!((int64_t)a->n_blocks * kTile * kTile < lim && (int64_t)((a->K + kTile - 1) / kTile) * kTile * d->ldb * 4 < lim &&
+          (int64_t)a->M * d->ldc * esz < lim))
+      return fail(VOID_ERR_UNSUPPORTED, "E4M3 x fp32 SpMM operands must stay below 2 GiB");
+    switch (d->out_dtype) {
+      case VOID_DT_F32: return launch_cg<kEltFp8F32, VOID_EPI_PER_BLOCK, VOID_DT_F32, false, true>(p, grid, stream);
+      case VOID_DT_BF16: return launch_cg<kEltFp8F32, VOID_EPI_PER_BLOCK, VOID_DT_BF16, false, true>(p, grid, stream);
+      case VOID_DT_F16: return launch_cg<kEltFp8F32, VOID_EPI_PER_BLOCK, VOID_DT_F16, false, true>(p, grid, stream);
+      default: return fail(VOID_ERR_UNSUPPORTED, "E4M3 x fp32 SpMM writes f32, bf16 or f16");
+    }
+  }
   if (elt == kEltF32) {
     const bool vec = c_ok && (bu % 16 == 0) && (d->ldb % 4 == 0) && (d->N % 4 == 0);
     // The column-group LDS-DMA ring for row-major B with 16-byte aligned rows,
@@ -2517,6 +2637,12 @@ int void_spmm_int8(const void_bsr_desc* a, const void_dense_args* d, int32_t epi
 int void_spmm_fp8(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
                   void* workspace, size_t workspace_bytes, hipStream_t stream) {
   return run(kEltFp8, a, d, VOID_EPI_PER_BLOCK, plan, workspace, workspace_bytes, stream);
+}
+
+int void_spmm_fp8_f32b(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
+                       void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (d && d->out_dtype == VOID_DT_I32) return fail(VOID_ERR_UNSUPPORTED, "E4M3 x fp32 SpMM writes f32, bf16 or f16");
+  return run(kEltFp8F32, a, d, VOID_EPI_PER_BLOCK, plan, workspace, workspace_bytes, stream);
 }
 
 int void_spmm_f32(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,

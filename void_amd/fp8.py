@@ -223,13 +223,16 @@ def void_spmm_fp8(a: FP8VOIDTensor, b: torch.Tensor, output_dtype: torch.dtype =
                   b_scale: Optional[Union[float, torch.Tensor]] = None, activation: str = "none",
                   bias: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                   chunk_tiles: Optional[int] = None) -> torch.Tensor:
-    """FP8 block-sparse SpMM C = A @ B (fp8.py:674-742) on the gfx950 fp8 MFMA kernel.
+    """FP8 block-sparse SpMM C = A @ B (fp8.py:674-742) on the gfx950 kernels.
 
-    B in float8_e4m3fn is used as given, multiplied by b_scale (default 1.0;
-    a scalar or N per-column scales).  A float B is first quantised per
-    tensor to E4M3 (its amax / 448 scale) — the reference instead keeps B
-    in fp32 for its TF32 dot, so this path carries B's quantisation error as
-    well.  Output dtype float32 / bfloat16 / float16.
+    A float B (fp32, bf16, fp16) keeps the reference's semantics: the kernel
+    computes sum_t s_t dec(A_t) @ B with B in fp32 (fp8.py:624-671 upcasts
+    both operands), here on the bf16 MFMA with A decoded exactly to bf16 and
+    B split into bf16 hi + lo (within 2^-16 relative per product).
+    A float8_e4m3fn B runs on the fp8 x fp8 MFMA and is taken as the codes'
+    values, as the reference's upcast does.
+    b_scale (default 1.0; a scalar or N per-column scales) multiplies the
+    result in either case.  Output dtype float32 / bfloat16 / float16.
     """
     if b.dim() != 2 or a.shape[1] != b.shape[0]:
         raise ValueError(f"B must be [K={a.shape[1]}, N], got {tuple(b.shape)}")
@@ -238,13 +241,11 @@ def void_spmm_fp8(a: FP8VOIDTensor, b: torch.Tensor, output_dtype: torch.dtype =
     if bias is not None and tuple(bias.shape) != (N,):
         raise ValueError(f"bias must be [{N}], got {tuple(bias.shape)}")
     _runtime.require_gpu(b, "B")
-    if b.dtype != torch.float8_e4m3fn:
-        if b.dtype == torch.float8_e5m2:
-            raise NotImplementedError("E5M2 B operands are not supported by the gfx950 kernel")
-        b, s = quantize_dense_fp8(b)
-        if b_scale is not None:
-            raise ValueError("b_scale is only meaningful for an already-quantised float8 B")
-        b_scale = s
+    if b.dtype == torch.float8_e5m2:
+        raise NotImplementedError("E5M2 B operands are not supported by the gfx950 kernels")
+    float_b = b.dtype != torch.float8_e4m3fn
+    if float_b and not b.is_floating_point():
+        raise TypeError(f"B must be float8_e4m3fn or a float tensor, got {b.dtype}")
     from .int_quant import _b_scale_args
     scalar_scale, scale_vec = _b_scale_args(b_scale, N, b.device)
     if out is None:
@@ -264,10 +265,32 @@ def void_spmm_fp8(a: FP8VOIDTensor, b: torch.Tensor, output_dtype: torch.dtype =
     if bias is not None:
         bias = bias.to(device=b.device, dtype=torch.float32).contiguous()
     chunk = chunk_tiles or tuning.select_chunk("fp8", a.n_blocks, N, a.device_bsr().max_row)
-    return _runtime.launch("fp8", a.device_bsr(), b.view(torch.uint8) if b.dim() == 2 else b,
-                           b_scale=scalar_scale, b_scale_vec=scale_vec, out=out,
-                           epilogue=_lib.EPI_PER_BLOCK, activation=get_activation_code(activation),
-                           bias=bias, chunk=chunk)
+    act = get_activation_code(activation)
+    if not float_b:
+        return _runtime.launch("fp8", a.device_bsr(), b.view(torch.uint8), b_scale=scalar_scale,
+                               b_scale_vec=scale_vec, out=out, epilogue=_lib.EPI_PER_BLOCK, activation=act,
+                               bias=bias, chunk=chunk)
+    if chunk > tuning.FP32_B_MAX_CHUNK:
+        raise ValueError(f"a float B takes chunk_tiles <= {tuning.FP32_B_MAX_CHUNK}, got {chunk}")
+    # fp32 B, row-major with 16-byte aligned rows and N % 4 == 0 (the ring
+    # kernel's layout); other widths run on zero-padded columns.
+    N4 = (N + 3) // 4 * 4
+    if N4 == N:
+        b32 = b.to(torch.float32).contiguous()
+        if b32.data_ptr() % 16:
+            b32 = b32.clone()
+        return _runtime.launch("fp8_f32b", a.device_bsr(), b32, b_scale=scalar_scale, b_scale_vec=scale_vec,
+                               out=out, epilogue=_lib.EPI_PER_BLOCK, activation=act, bias=bias, chunk=chunk)
+    b32 = torch.zeros(K, N4, dtype=torch.float32, device=b.device)
+    b32[:, :N] = b
+    pad = lambda v, fill: torch.cat([v, torch.full((N4 - N,), fill, dtype=v.dtype, device=v.device)])
+    wide = torch.empty(M, N4, dtype=output_dtype, device=b.device)
+    _runtime.launch("fp8_f32b", a.device_bsr(), b32, b_scale=scalar_scale,
+                    b_scale_vec=None if scale_vec is None else pad(scale_vec, 1.0), out=wide,
+                    epilogue=_lib.EPI_PER_BLOCK, activation=act, bias=None if bias is None else pad(bias, 0.0),
+                    chunk=chunk)
+    out.copy_(wide[:, :N])
+    return out
 
 
 def void_tensor_to_fp8(void_tensor, format: str = "e4m3", scale_mode: str = "per_block") -> FP8VOIDTensor:

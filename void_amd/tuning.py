@@ -43,6 +43,11 @@ CHUNK_TABLE = {
 }
 
 
+# Longest work item of the kernels that stage fp32 B slabs (the float SpMM
+# and the E4M3 x fp32 SpMM): they hold an item's block columns one per lane.
+FP32_B_MAX_CHUNK = 64
+
+
 def resident_workgroups() -> int:
     return GFX950_CUS * WORKGROUPS_PER_CU
 
