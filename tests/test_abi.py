@@ -247,3 +247,46 @@ def test_csr_conversion_argument_checks():
     assert lib.void_csr_count_blocks(None, None, 10, 10, None, 0, None, None) == -1
     assert lib.void_csr_to_tiles(None, None, None, 10, 10, None, 0, 0, None, None, None, None, None) == 0
     assert lib.void_csr_to_tiles(None, None, None, 10, 10, None, 0, 1, None, None, None, None, None) == -1
+
+
+def test_plan_from_workload_covers_every_tile_once():
+    # void_spmm_stream_k runs a workload's worker ranges as work items: every
+    # tile of every row exactly once, split rows numbered densely, rows
+    # without workers still present (empty items), items of at most 64 tiles.
+    from void_amd import _runtime
+    from void_amd.stream_k import StreamKWorkload
+    rng = np.random.default_rng(3)
+    counts = np.minimum(rng.zipf(1.5, 200), 300)
+    counts[5] = 0
+    rp = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    ci = rng.integers(0, 512, rp[-1]).astype(np.int32)
+    vt = None
+    rows, begins, ends = [], [], []
+    for r in range(200):
+        if r == 7:
+            continue  # a row the workload leaves out
+        b, e = rp[r], rp[r + 1]
+        step = 16
+        for s in range(b, e, step):
+            rows.append(r), begins.append(s), ends.append(min(e, s + step))
+    items, n_split, n_slots, longest = _runtime.plan_from_ranges(rp, ci, np.array(rows), np.array(begins),
+                                                                  np.array(ends), 64)
+    assert longest <= 64
+    seen = np.zeros(rp[-1], np.int32)
+    for it in items:
+        seen[it[1]:it[2]] += 1
+        m = min(it[2] - it[1], 24)
+        assert np.array_equal(it[8:8 + m], ci[it[1]:it[1] + m])
+    expect = np.ones(rp[-1], np.int32)
+    expect[rp[7]:rp[8]] = 0
+    assert np.array_equal(seen, expect)
+    assert set(items[:, 0]) == set(range(200))
+    split = items[items[:, 3] >= 0]
+    assert sorted(set(split[:, 3])) == list(range(n_split))
+    assert n_slots == len(split)
+    for t in range(n_split):
+        ch = split[split[:, 3] == t]
+        assert sorted(ch[:, 5]) == list(range(len(ch))) and np.all(ch[:, 4] == len(ch))
+        assert len(set(ch[:, 6])) == 1
+    with pytest.raises(ValueError):
+        _runtime.plan_from_ranges(rp, ci, np.array([0]), np.array([rp[0]]), np.array([rp[2]]), 64)

@@ -50,7 +50,7 @@ from .fusion import (ActivationType, FusedOpType, FusedSparseLinear, FusedSparse
 from .packed import load_packed, pack, save_packed, unpack
 from .ops import void_spmm
 from .autograd import SparseLinear, VOIDSpMM, VOIDSpMMFunction
-from .stream_k import StreamKWorkload, analyze_workload_balance, compute_stream_k_workload
+from .stream_k import StreamKWorkload, analyze_workload_balance, compute_stream_k_workload, void_spmm_stream_k
 
 __version__ = "0.1.0"
 
@@ -63,5 +63,5 @@ __all__ = [
     "FP8Format", "FP8Config", "FP8ScalingInfo", "FP8VOIDTensor", "create_scaling_info", "compute_amax",
     "quantize_to_fp8", "dequantize_from_fp8", "void_spmm_fp8", "void_tensor_to_fp8",
     "ActivationType", "get_activation_code", "void_spmm_gelu", "void_spmm_relu", "void_spmm_silu",
-    "StreamKWorkload", "compute_stream_k_workload", "analyze_workload_balance",
+    "StreamKWorkload", "compute_stream_k_workload", "analyze_workload_balance", "void_spmm_stream_k",
 ]

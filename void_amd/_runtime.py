@@ -103,6 +103,67 @@ def plan_rows(row_ptr_host: np.ndarray, chunk: int,
     return items, n_tiles.value, n_slots.value
 
 
+def plan_from_ranges(row_ptr_host: np.ndarray, col_idx_host: np.ndarray, rows: np.ndarray, begins: np.ndarray,
+                     ends: np.ndarray, max_chunk: int) -> Tuple[np.ndarray, int, int, int]:
+    """Work items that run exactly the given tile ranges (BSR positions
+    [begins[w], ends[w]) of block-row rows[w]), as the reference's Stream-K
+    workers do (stream_k.py:113-222).
+
+    Ranges longer than max_chunk are cut into near-equal pieces.  A row
+    covered by more than one range becomes a split row whose partial blocks
+    the kernel sums in range order; rows that no range covers get an empty
+    item, so their output is written (zero, or the epilogue of zero), where
+    the reference leaves its zero-filled output untouched.
+    Returns (items[n, 32] int32, n_split_tiles, n_slots, longest item)."""
+    rp = np.asarray(row_ptr_host, dtype=np.int64)
+    n_br = rp.size - 1
+    rows = np.asarray(rows, dtype=np.int64).reshape(-1)
+    begins = np.asarray(begins, dtype=np.int64).reshape(-1)
+    ends = np.asarray(ends, dtype=np.int64).reshape(-1)
+    if not (rows.size == begins.size == ends.size):
+        raise ValueError("worker_rows, worker_block_start and worker_block_end differ in length")
+    if rows.size and (rows.min() < 0 or rows.max() >= n_br):
+        raise ValueError(f"worker rows must lie in [0, {n_br})")
+    if np.any(begins > ends) or np.any(begins < rp[rows]) or np.any(ends > rp[rows + 1]):
+        raise ValueError("a worker's block range lies outside its block-row")
+    pieces = []  # (row, begin, end)
+    for r, b, e in zip(rows.tolist(), begins.tolist(), ends.tolist()):
+        n = e - b
+        if n == 0:
+            continue
+        k = -(-n // max_chunk)
+        for c in range(k):
+            pieces.append((r, b + c * n // k, b + (c + 1) * n // k))
+    pieces.sort(key=lambda x: (x[0], x[1]))
+    covered = np.zeros(n_br, dtype=bool)
+    per_row = {}
+    for pc in pieces:
+        per_row.setdefault(pc[0], []).append(pc)
+        covered[pc[0]] = True
+    W = _lib.ITEM_INTS
+    items = []
+    n_tiles = n_slots = 0
+    ci = np.asarray(col_idx_host, dtype=np.int32)
+    for r in range(n_br):
+        lst = per_row.get(r)
+        if not lst:
+            lst = [(r, int(rp[r]), int(rp[r]))]
+        split = len(lst) > 1
+        for c, (_, b, e) in enumerate(lst):
+            it = np.full(W, -1, dtype=np.int32)
+            it[:8] = (r, b, e, n_tiles if split else -1, len(lst), c if split else 0, n_slots if split else 0, 0)
+            m = min(e - b, _lib.ITEM_INLINE_COLS)
+            it[8:8 + m] = ci[b:b + m]
+            items.append(it)
+        if split:
+            n_tiles += 1
+            n_slots += len(lst)
+    arr = np.stack(items).astype(np.int32)
+    lengths = arr[:, 2] - arr[:, 1]
+    arr = arr[np.argsort(-lengths, kind="stable")]  # longest first, as the planner orders
+    return arr, n_tiles, n_slots, int(lengths.max()) if lengths.size else 0
+
+
 @dataclass
 class DeviceBsr:
     tiles: torch.Tensor          # uint8 [n_blocks, 32, 32] block-row-major

@@ -16,10 +16,12 @@ F32_CHUNK = 64
 
 
 def float_spmm(a, b: torch.Tensor, *, out: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
-               activation: int = _lib.ACT_NONE, bias_per_row: bool = False) -> torch.Tensor:
+               activation: int = _lib.ACT_NONE, bias_per_row: bool = False,
+               plan: Optional["_runtime.DevicePlan"] = None) -> torch.Tensor:
     """activation(A @ B + bias) for a float VOIDTensor A; the output has B's
     dtype (f32, bf16 or f16), as the reference's kernels write.  bias is [N]
-    (per column), or [M] with bias_per_row (fusion.py:202-304)."""
+    (per column), or [M] with bias_per_row (fusion.py:202-304).  ``plan``
+    (work items of at most 64 tiles) replaces the default partition."""
     if b.dim() != 2:
         raise ValueError("B must be 2-D")
     M, K = a.shape
@@ -48,7 +50,10 @@ def float_spmm(a, b: torch.Tensor, *, out: Optional[torch.Tensor] = None, bias: 
     dbsr = a.device_bsr()
     lib = _lib.lib()
     target = out if (out.stride(1) == 1 and out.stride(0) >= N) else torch.empty_like(out)
-    plan = dbsr.plan(F32_CHUNK)
+    if plan is None:
+        plan = dbsr.plan(F32_CHUNK)
+    elif plan.chunk > F32_CHUNK:
+        raise ValueError(f"the float kernel takes work items of at most {F32_CHUNK} tiles, got {plan.chunk}")
     ws, ws_bytes = plan.workspace(N, out.device)
     cplan = _lib.Plan(items=plan.items.data_ptr(), n_items=plan.n_items, n_split_tiles=plan.n_split_tiles,
                       n_slots=plan.n_slots, chunk_tiles=plan.chunk)

@@ -88,4 +88,55 @@ def analyze_workload_balance(void_tensor) -> dict:
     }
 
 
-__all__ = ["StreamKWorkload", "compute_stream_k_workload", "analyze_workload_balance"]
+def workload_plan(void_tensor, workload: StreamKWorkload) -> "_runtime.DevicePlan":
+    """Device work items that run exactly the workload's worker ranges,
+    cached on the tensor's device view per workload object."""
+    from .ops import F32_CHUNK
+    dbsr = void_tensor.device_bsr()
+    key = ("workload", id(workload))
+    cached = dbsr.plans.get(key)
+    if cached is not None and cached[0] is workload:
+        return cached[1]
+    items, n_tiles, n_slots, longest = _runtime.plan_from_ranges(
+        dbsr.row_ptr_host, dbsr.col_idx_host, workload.worker_rows.detach().cpu().numpy(),
+        workload.worker_block_start.detach().cpu().numpy(), workload.worker_block_end.detach().cpu().numpy(),
+        F32_CHUNK)
+    plan = _runtime.DevicePlan(torch.from_numpy(items).to(dbsr.row_ptr.device), items.shape[0], n_tiles, n_slots,
+                               max(longest, 1), items)
+    old = [k for k in dbsr.plans if isinstance(k, tuple) and k[0] == "workload"]
+    for k in old[:max(0, len(old) - 7)]:  # keep the plans of the last 8 workloads
+        del dbsr.plans[k]
+    dbsr.plans[key] = (workload, plan)
+    return plan
+
+
+def void_spmm_stream_k(a, b: torch.Tensor, workload: Optional[StreamKWorkload] = None,
+                       out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Stream-K load-balanced SpMM C = A @ B for a float VOIDTensor
+    (stream_k.py:233-301), on the fp32 MFMA kernel of libvoid_amd.so.
+
+    Each worker of ``workload`` (computed by compute_stream_k_workload when
+    None) becomes one work item over its tile range; the partial blocks of a
+    row that several workers share are summed in range order by the last of
+    them to finish (a deterministic fix-up in place of the reference's
+    spin-locked read-modify-write).  C has B's dtype; ``out`` is
+    overwritten."""
+    if b.dim() != 2 or a.shape[1] != b.shape[0]:
+        raise ValueError(f"B must be [K={a.shape[1]}, N], got {tuple(b.shape)}")
+    _runtime.require_gpu(b, "B")
+    _runtime.require_gpu(a.values, "A")
+    from .ops import float_spmm
+    M, N = a.shape[0], b.shape[1]
+    if out is not None and tuple(out.shape) != (M, N):
+        raise ValueError(f"out must be [{M}, {N}]")
+    if a.n_blocks == 0:
+        if out is None:
+            return torch.zeros(M, N, dtype=b.dtype, device=b.device)
+        return out.zero_()
+    if workload is None:
+        workload = compute_stream_k_workload(a)
+    return float_spmm(a, b, out=out, plan=workload_plan(a, workload))
+
+
+__all__ = ["StreamKWorkload", "compute_stream_k_workload", "analyze_workload_balance", "void_spmm_stream_k",
+           "workload_plan"]
