@@ -91,6 +91,7 @@ struct Params {
   int32_t item_piles;   // XCDs among which one panel group's items are dealt (see wg_map)
   int32_t xcd_exact;    // grid laid out per XCD (see wg_map)
   int32_t bias_per_row;  // float kernel: bias indexed by output row
+  int32_t pair_snake;    // exact layout: second half of an XCD's share reversed (see wg_map)
 };
 
 #ifdef VOID_TRACE
@@ -101,9 +102,11 @@ struct Params {
 #define TRACE_POINT(k) asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(tr##k))
 #define TRACE_TAG(v)                                                           \
   do {                                                                         \
-    unsigned x_;                                                               \
+    unsigned x_, h_;                                                           \
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x_));          \
-    tr7 = (unsigned long long)(v) | ((unsigned long long)(x_ & 15) << 8);      \
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(h_));           \
+    tr7 = (unsigned long long)(v) | ((unsigned long long)(x_ & 15) << 8) |     \
+          ((unsigned long long)h_ << 40);                                      \
   } while (0)
 #define TRACE_FLUSH()                                                              \
   do {                                                                             \
@@ -190,7 +193,14 @@ __device__ __forceinline__ void wg_tile(int L, int n_items, int n_panels, int pg
 // runs every item_piles-th item of the longest-first list, starting at item
 // x % item_piles, one whole item (its panel_group panels back to back) after
 // another.  The grid is 8 x (that share's workgroups, rounded up), so every
-// XCD's share is a longest-first slice of equal length.
+// XCD's share is a longest-first slice of equal length.  Unsplit grids of
+// one resident round (pair_snake) take the same layout with the second half
+// of each XCD's share reversed: the dispatcher gives each CU of an XCD one
+// workgroup of the first half and then one of the second (read from
+// HW_REG_HW_ID in an instrumented build: workgroups s and s + 32 of an XCD's
+// 64 share a CU), so a CU's pair is a long and a short row.  Against
+// contiguous ranges, where one XCD of a panel took all its longest rows, c2
+// went 8.6-8.8 -> 7.9-8.1 us and c3 10.9-11.1 -> 10.2-10.7 us cold.
 // Otherwise each XCD runs a contiguous range of logical ids (xcd_remap),
 // mapped by wg_tile.
 __device__ __forceinline__ bool wg_map(const Params& p, int& item, int& panel) {
@@ -198,8 +208,12 @@ __device__ __forceinline__ bool wg_map(const Params& p, int& item, int& panel) {
   if (p.xcd_exact) {
     const int x = h & 7, s = h >> 3;
     const int piles = p.item_piles, pg = p.panel_group;
-    const int k = s / pg;
+    int k = s / pg;
     panel = (x / piles) * pg + (s - k * pg);
+    if (p.pair_snake) {
+      const int share = (p.n_items + piles - 1) / piles, half = (share + 1) >> 1;
+      k = k < half ? k : share - 1 - (k - half);
+    }
     item = k * piles + x % piles;
     return item < p.n_items;
   }
@@ -2337,7 +2351,14 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
   {
     const int n_groups = (n_panels + p.panel_group - 1) / p.panel_group;
     p.item_piles = n_split_tiles > 0 ? std::max(1, 8 / n_groups) : 1;
-    if (n_split_tiles > 0 && n_panels % p.panel_group == 0 && 8 % n_groups == 0) {
+    // One-round unsplit grids (every workgroup resident from the start) take
+    // the same dealt layout, with the second half of each XCD's share in
+    // reverse: a CU's two workgroups are then one long and one short row.
+    if (n_split_tiles == 0 && grid64 <= kPairGridMax) {
+      p.item_piles = std::max(1, 8 / n_groups);
+      p.pair_snake = 1;
+    }
+    if ((n_split_tiles > 0 || p.pair_snake) && n_panels % p.panel_group == 0 && 8 % n_groups == 0) {
       p.xcd_exact = 1;
       grid_exact = 8 * (((int64_t)n_items + p.item_piles - 1) / p.item_piles) * p.panel_group;
     }
