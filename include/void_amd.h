@@ -171,6 +171,25 @@ int void_spmm_int8(const void_bsr_desc* a, const void_dense_args* d, int32_t epi
                    const void_plan* plan, void* workspace, size_t workspace_bytes,
                    hipStream_t stream);
 
+/* void_spmm_int8 without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  It
+ * calls no hipMalloc, hipFree or allocating library routine: the split-row
+ * counters and partial blocks live in a static device array of the library
+ * (32 MiB per GPU, held from module load to process end).  A plan may need
+ * at most VOID_NOALLOC_COUNTER_BYTES of counters (counters_bytes: n_split_tiles
+ * x ceil(N / 128) x 4, rounded up to 256) and VOID_NOALLOC_PARTIAL_BYTES of
+ * partials (void_workspace_bytes minus the counters); larger plans fail with
+ * VOID_ERR_WORKSPACE.  The first call on a device that splits rows looks the
+ * array up and clears its counters with a kernel on `stream`.  All calls on
+ * one GPU share the array: calls that overlap in time on one GPU race (run
+ * them on one stream, or use void_spmm_int8 with a workspace per stream).
+ * Results are identical to void_spmm_int8's. */
+#define VOID_NOALLOC_COUNTER_BYTES ((size_t)1 << 20)
+#define VOID_NOALLOC_PARTIAL_BYTES (((size_t)31) << 20)
+int void_spmm_int8_noalloc(const void_bsr_desc* a, const void_dense_args* d, int32_t epilogue,
+                           const void_plan* plan, hipStream_t stream);
+
 /* FP8 (E4M3FN x E4M3FN, fp32 accumulate) block-sparse SpMM, replacing
  * void_spmm_fp8_kernel + void_spmm_fp8 (void/fp8.py:577-742).  The epilogue
  * is always PER_BLOCK: C = s_b * sum_t s_a[t] * (A_t @ B_t). */

@@ -14,6 +14,10 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().with_name("libvoid_amd.so")
 ABI_VERSION = 3
 
+# Scratch limits of void_spmm_int8_noalloc (VOID_NOALLOC_*_BYTES)
+NOALLOC_COUNTER_BYTES = 1 << 20
+NOALLOC_PARTIAL_BYTES = 31 << 20
+
 # enum void_epilogue
 EPI_RAW_I32 = 0
 EPI_ROW_MEAN = 1
@@ -102,6 +106,7 @@ SIGNATURES = {
     "void_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
     "void_spmm_int8": (c_int, [POINTER(BsrDesc), POINTER(DenseArgs), c_int32, POINTER(Plan),
                                c_void_p, c_size_t, c_void_p]),
+    "void_spmm_int8_noalloc": (c_int, [POINTER(BsrDesc), POINTER(DenseArgs), c_int32, POINTER(Plan), c_void_p]),
     "void_spmm_fp8": (c_int, [POINTER(BsrDesc), POINTER(DenseArgs), POINTER(Plan),
                               c_void_p, c_size_t, c_void_p]),
     "void_spmm_fp8_f32b": (c_int, [POINTER(BsrDesc), POINTER(DenseArgs), POINTER(Plan),

@@ -36,6 +36,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <type_traits>
 #include <vector>
 
@@ -2285,8 +2286,18 @@ int n_panels_for(int32_t N) { return (N + kPanel - 1) / kPanel; }
 
 unsigned long long* g_trace = nullptr;  // set by void_debug_set_trace in instrumented builds
 
+// Split-row counters and partials at fixed places (the allocation-free entry
+// point's scratch) in place of a caller's workspace.
+struct FixedScratch {
+  unsigned* counters;
+  size_t counter_bytes;
+  void* partials;
+  size_t partial_bytes;
+};
+
 int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilogue,
-        const void_plan* plan, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+        const void_plan* plan, void* workspace, size_t workspace_bytes, hipStream_t stream,
+        const FixedScratch* fixed = nullptr) {
   g_err[0] = 0;
   if (!a || !d || !plan) return fail(VOID_ERR_ARG, "null descriptor or plan");
   const void_work_item* items = plan->items;
@@ -2366,7 +2377,17 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
   p.bias_per_row = d->bias_per_row;
   p.items = items;
   p.trace = g_trace;
-  if (n_split_tiles > 0) {
+  if (n_split_tiles > 0 && fixed) {
+    const size_t need_c = counters_bytes(n_split_tiles, n_panels);
+    const size_t need_p = void_workspace_bytes(n_split_tiles, plan->n_slots, d->N) - need_c;
+    if (need_c > fixed->counter_bytes || need_p > fixed->partial_bytes)
+      return fail(VOID_ERR_WORKSPACE,
+                  "plan needs %zu bytes of split-row counters and %zu of partials; the allocation-free "
+                  "entry point holds at most %zu and %zu (use void_spmm_int8 with a workspace)",
+                  need_c, need_p, fixed->counter_bytes, fixed->partial_bytes);
+    p.counters = fixed->counters;
+    p.partials = fixed->partials;
+  } else if (n_split_tiles > 0) {
     if (!workspace) return fail(VOID_ERR_WORKSPACE, "plan splits rows but workspace is null");
     const size_t need = void_workspace_bytes(n_split_tiles, plan->n_slots, d->N);
     if (workspace_bytes < need)
@@ -2556,6 +2577,58 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
   return launch_out<kEltFp8, VOID_EPI_PER_BLOCK>(p, grid, stream, layout, d->out_dtype);
 }
 
+// ---- Scratch of the allocation-free entry point ---------------------------
+//
+// The split-row counters and partial blocks of void_spmm_int8_noalloc live in
+// this array, which every GPU the library runs on holds from module load to
+// process end.  Counters take the first kScratchCounterBytes (up to 262144
+// split (tile, panel) pairs), partials the rest, so a plan's partials never
+// overlap another plan's counters.  The split-row protocol leaves every
+// counter it used at zero, so the region is cleared once per device, at set-up.
+// In host code `scratch` is a host-side stand-in, not the device address;
+// only the pointer from hipGetSymbolAddress (g_scratch_ptr) is used.
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+constexpr size_t kScratchCounterBytes = (size_t)1 << 20;
+static_assert(kScratchCounterBytes == VOID_NOALLOC_COUNTER_BYTES &&
+                  kScratchBytes - kScratchCounterBytes == VOID_NOALLOC_PARTIAL_BYTES,
+              "limits stated in void_amd.h");
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+__global__ __launch_bounds__(256) void zero_words_kernel(unsigned* p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// The scratch address on the current device, looked up (and its counter
+// region cleared, on `stream`) at the first call on that device.
+int scratch_for_current_device(hipStream_t stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(VOID_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(VOID_ERR_HIP, "device %d beyond the scratch table", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(VOID_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    // A fill kernel, not hipMemsetAsync, so that set-up under graph capture
+    // records a kernel node.
+    const int words = (int)(kScratchCounterBytes / sizeof(unsigned));
+    hipLaunchKernelGGL(zero_words_kernel, dim3((words + 255) / 256), dim3(256), 0, stream,
+                       static_cast<unsigned*>(ptr), words);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(VOID_ERR_HIP, "scratch clear: %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return VOID_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -2653,6 +2726,23 @@ int void_spmm_int8(const void_bsr_desc* a, const void_dense_args* d, int32_t epi
                    const void_plan* plan, void* workspace, size_t workspace_bytes,
                    hipStream_t stream) {
   return run(kEltI8, a, d, epilogue, plan, workspace, workspace_bytes, stream);
+}
+
+int void_spmm_int8_noalloc(const void_bsr_desc* a, const void_dense_args* d, int32_t epilogue,
+                           const void_plan* plan, hipStream_t stream) {
+  g_err[0] = 0;
+  if (!plan) return fail(VOID_ERR_ARG, "null plan");
+  FixedScratch fs{};
+  if (plan->n_split_tiles > 0) {
+    void* base = nullptr;
+    const int rc = scratch_for_current_device(stream, &base);
+    if (rc != VOID_OK) return rc;
+    fs.counters = static_cast<unsigned*>(base);
+    fs.counter_bytes = kScratchCounterBytes;
+    fs.partials = static_cast<char*>(base) + kScratchCounterBytes;
+    fs.partial_bytes = kScratchBytes - kScratchCounterBytes;
+  }
+  return run(kEltI8, a, d, epilogue, plan, nullptr, 0, stream, &fs);
 }
 
 int void_spmm_fp8(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
