@@ -1415,6 +1415,14 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
         dma_b128(da, &a_ring[slot0 + wave][0], live ? voff_a : kOutOfRange,
                  (begin + (live ? idx : 0)) * (kTile * kTile));
       }
+      // A live stage with K % 32 == 0 (no slab crosses K) needs no per-tile
+      // offset selects.
+      if (base + RT <= nt && kb_last < 0) {
+#pragma unroll
+        for (int u = 0; u < RT; ++u)
+          dma_b128(db, &b_ring[slot0 + u][wave * (kSlotBytes / kWaves)], voffd, stage_col(s, u) * b_kstride);
+        return;
+      }
 #pragma unroll
       for (int u = 0; u < RT; ++u) {
         const int kb = stage_col(s, u);
@@ -1513,9 +1521,15 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
         const float sc = bcast(scw, base);
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] = __builtin_fmaf(sc, part[r], acc[r]);
-      } else if (base + RT <= nt) {
-        // A full stage: all operand reads first, then four independent
-        // products, so that one tile's scaling overlaps the next MFMA.
+      } else {
+        // Every stage runs as a full one: all operand reads first, then RT
+        // independent products, so that one tile's scaling overlaps the next
+        // MFMA.  The slots of tiles past the item's end were loaded out of
+        // range, which writes zeros to LDS, so their integer products are
+        // zero; the per-block fold also gives them a zero scale.  One code
+        // path keeps the accumulators in place: with a separate path for
+        // the item's last, partial stage the compiler copied all 16 of them
+        // twice per stage (16 v_mov_b64 per 3-tile stage on c5).
         Frag1 f[RT];
 #pragma unroll
         for (int u = 0; u < RT; ++u) {
@@ -1535,17 +1549,10 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
           for (int u = 0; u < RT; ++u) {
             __builtin_amdgcn_sched_barrier(0);
             if (u + 2 < RT) part[u + 2] = A::prod(f[u + 2]);
-            A::fold(acc, part[u], bcast(scw, base + u));
-          }
-        }
-      } else {
-#pragma unroll
-        for (int u = 0; u < RT; ++u) {
-          if (base + u < nt) {
-            Frag1 f;
-            f.a = a_ring[slot0 + u][lane];
-            f.b = read_tr(&b_ring[slot0 + u][0], wave, j, g);
-            A::step(acc, f, kScales ? bcast(scw, base + u) : 0.f);
+            // The select on the scale's bits stays in SGPRs (a float select
+            // compiled to v_mov + v_cndmask per tile).
+            const int si = __builtin_amdgcn_readlane(__float_as_int(scw), min(base + u, kCgMaxTiles - 1));
+            A::fold(acc, part[u], __int_as_float(base + u < nt ? si : 0));
           }
         }
       }
