@@ -43,7 +43,7 @@ BF16_PEAK_TFLOPS = 2500.0  # dense MFMA bf16, MI355X
 # FETCH_SIZE and WRITE_SIZE in separate runs of `bench.py --counters`, each
 # scaled by what the same counter reads for a plain 64 MiB copy (FETCH x 1.9993,
 # WRITE x 1.0).  Workloads not listed here report null.
-MEASURED_TRAFFIC = {"c2": 19725950, "c3": 22299452, "c4": 91278739, "c5": 187438356}
+MEASURED_TRAFFIC = {"c2": 19682436, "c3": 22283060, "c4": 91217453, "c5": 186818873}
 
 
 def parse():
