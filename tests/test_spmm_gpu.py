@@ -205,6 +205,35 @@ def test_c5_ffn_full_sampled_rows(gpu, monkeypatch):
     assert np.all(err <= 2.0 ** -8 * np.abs(ref) + 1e-4), err.max()
 
 
+def test_c5_row_group_kernel_full(gpu, monkeypatch):
+    """Config 5 at full size on the row-group kernel (VOID_AMD_KERNEL=rg):
+    the int32 accumulators of the whole output equal the column-group
+    kernel's (both exact), and the per-block GELU output of sampled rows
+    matches the oracle within bf16 rounding."""
+    case = cases.c5_ffn()
+    qd, A, bq, bs = _int8_setup(case, gpu)
+    bt, st = torch.from_numpy(bq).to(gpu), torch.from_numpy(bs).to(gpu)
+    monkeypatch.setenv("VOID_AMD_KERNEL", "rg")
+    assert qd.device_bsr().use_row_groups(case.N)
+    raw = void_amd.void_spmm_int8(qd, bt, b_scale=st, epilogue="raw_i32")
+    out = void_amd.void_spmm_gelu(qd, bt, b_scale=st, out_dtype=torch.bfloat16, epilogue="per_block")
+    monkeypatch.delenv("VOID_AMD_KERNEL")
+    raw_cg = void_amd.void_spmm_int8(qd, bt, b_scale=st, epilogue="raw_i32")
+    torch.cuda.synchronize()
+    assert torch.equal(raw, raw_cg)
+    rows = np.array([0, 7, 8, 100, 223, 447])
+    where = np.full(len(A.row_ptr) - 1, -1)
+    where[rows] = np.arange(len(rows))
+    keep = where[case.block_rows] >= 0
+    q = void_amd.quantize_void_tensor(cases.make_void_tensor(case, "cpu"))
+    sub = oracle.Bsr(q.values.numpy()[keep], q.scales.numpy()[keep], where[case.block_rows[keep]],
+                     case.block_cols[keep], (len(rows) * 32, case.K))
+    sel = (rows[:, None] * 32 + np.arange(32)[None, :]).reshape(-1)
+    ref = oracle.gelu_tanh(oracle.i8_per_block(sub, bq, bs))
+    err = np.abs(out.float().cpu().numpy()[sel] - ref)
+    assert np.all(err <= 2.0 ** -8 * np.abs(ref) + 1e-4), err.max()
+
+
 @pytest.mark.parametrize("chunk", [1, 3, 8, 100])
 def test_forced_split_row_mean_and_per_block(gpu, chunk, kernel):
     case = cases.uniform_blocks(1024, 2048, 256, 900, seed=3)
