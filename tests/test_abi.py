@@ -373,3 +373,17 @@ def test_rowgroup_plan_rejects_unsorted_columns():
     ci = np.array([5, 3], np.int32)
     with pytest.raises(_lib.VoidLibraryError):
         _runtime.plan_row_groups(rp, ci)
+
+
+def test_row_groups_not_planned_by_default(monkeypatch):
+    # The default path never runs the row-group planner, and a plan the
+    # planner rejects (block columns beyond 16 bits) falls back quietly.
+    rp = np.array([0, 1], np.int32)
+    ci = np.array([70000], np.int32)
+    d = _runtime.DeviceBsr(tiles=torch.zeros(1, 32, 32, dtype=torch.uint8), scales=torch.ones(1),
+                           row_ptr=torch.from_numpy(rp), col_idx=torch.from_numpy(ci), row_ptr_host=rp,
+                           col_idx_host=ci, per_tensor=False, M=32, K=70001 * 32, n_blocks=1, n_block_rows=1)
+    monkeypatch.delenv("VOID_AMD_KERNEL", raising=False)
+    assert not d.use_row_groups(128) and d._row_groups is None
+    monkeypatch.setenv("VOID_AMD_KERNEL", "rg")
+    assert not d.use_row_groups(128)

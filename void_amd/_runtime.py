@@ -248,7 +248,12 @@ class DeviceBsr:
         force = os.environ.get("VOID_AMD_KERNEL")
         if force and force != "rg":
             return False
-        rg = self.row_groups()
+        if force != "rg" and tuning.ROW_GROUP_MIN_SHARING == float("inf"):
+            return False  # off by default: no planning on the default path
+        try:
+            rg = self.row_groups()
+        except _lib.VoidLibraryError:
+            return False  # e.g. block columns beyond the plan's 16 bits: the column-group kernels run
         if force == "rg":
             return rg.max_stages <= tuning.ROW_GROUP_MAX_STAGES
         return tuning.use_row_groups(self.n_blocks, rg.n_steps, rg.n_groups, N, rg.max_stages)
