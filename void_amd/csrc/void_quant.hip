@@ -2,11 +2,12 @@
 // input side: per-tile symmetric INT8 (quantize_void_tensor) and per-tile
 // E4M3 (void_tensor_to_fp8), declared in include/void_amd.h.
 //
-// One wave64 per 32x32 fp32 tile: each lane loads 16 consecutive values (four
-// 16-byte loads, so one tile is one contiguous 4 KB read), the wave reduces
-// the tile's amax with cross-lane max, and every lane writes its 16 codes as
-// one 16-byte store.  The work is HBM-bound byte traffic: 4 KB in, 1 KB + 4
-// bytes out per tile.  Rounding follows the reference's torch arithmetic
+// One wave64 per 32x32 fp32 tile: load q (0..3) of lane l reads values
+// 256 q + 4 l .. + 3, so each load instruction reads 1 KB contiguously and
+// requests every cache line once; the wave reduces the tile's amax with
+// cross-lane max, and store q writes the lane's 4 codes of those values (256
+// contiguous bytes per instruction).  The work is HBM-bound byte traffic:
+// 4 KB in, 1 KB + 4 bytes out per tile.  Rounding follows the reference's torch arithmetic
 // exactly: IEEE fp32 division and multiplication, round half to even.
 
 #include <hip/hip_runtime.h>
@@ -31,14 +32,15 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// Loads this lane's 16 values of tile t and returns the tile's amax
-// (max |x|, which equals max(|min|, |max|) for finite values).
+// Loads this lane's 16 values of tile t (x[4 q + i] = value 256 q + 4 lane +
+// i) and returns the tile's amax (max |x|, which equals max(|min|, |max|) for
+// finite values).
 __device__ __forceinline__ float load_tile(const float* tiles, int64_t t, int lane, float (&x)[16]) {
-  const v4f* p = reinterpret_cast<const v4f*>(tiles + t * kTileElems) + lane * 4;
+  const v4f* p = reinterpret_cast<const v4f*>(tiles + t * kTileElems) + lane;
   float m = 0.f;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const v4f v = p[q];
+    const v4f v = __builtin_nontemporal_load(p + 64 * q);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       x[4 * q + i] = v[i];
@@ -51,6 +53,17 @@ __device__ __forceinline__ float load_tile(const float* tiles, int64_t t, int la
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
   return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
          ((uint32_t)(d & 0xff) << 24);
+}
+
+// Codes of this lane's 16 values (the layout of load_tile) into the tile's
+// 1 KB of codes: store w writes values 256 w + 4 lane .. + 3.
+template <class C>
+__device__ __forceinline__ void store_codes(void* dst, int lane, const C (&c)[16]) {
+  uint32_t* d = reinterpret_cast<uint32_t*>(dst) + lane;
+#pragma unroll
+  for (int w = 0; w < 4; ++w)
+    __builtin_nontemporal_store(pack4((int)c[4 * w], (int)c[4 * w + 1], (int)c[4 * w + 2], (int)c[4 * w + 3]),
+                                d + 64 * w);
 }
 
 // int_quant.py:178-214 (symmetric min/max scale), :254-305 (quantize_tensor):
@@ -67,10 +80,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void quantize_i8_kernel(const 
   int c[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) c[i] = (int)fminf(fmaxf(rintf(__fdiv_rn(x[i], s)), -128.0f), 127.0f);
-  v4i out;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) out[w] = (int)pack4(c[4 * w], c[4 * w + 1], c[4 * w + 2], c[4 * w + 3]);
-  *reinterpret_cast<v4i*>(q + t * kTileElems + lane * 16) = out;
+  store_codes(q + t * kTileElems, lane, c);
   if (lane == 0) scales[t] = s;
 }
 
@@ -117,10 +127,7 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void quantize_fp8_kernel(const
   uint32_t c[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) c[i] = e4m3_code(fminf(fmaxf(__fmul_rn(x[i], inv), -448.0f), 448.0f));
-  v4i out;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) out[w] = (int)pack4(c[4 * w], c[4 * w + 1], c[4 * w + 2], c[4 * w + 3]);
-  *reinterpret_cast<v4i*>(q + t * kTileElems + lane * 16) = out;
+  store_codes(q + t * kTileElems, lane, c);
   if (lane == 0) {
     scales[t] = s;
     if (amaxes) amaxes[t] = amax;
