@@ -116,6 +116,21 @@ __device__ __forceinline__ uint64_t spread_even(uint32_t v) {
   return x;
 }
 
+// Streaming (nontemporal) 16-byte accesses: data touched once per pass.
+typedef int nt_v4i __attribute__((ext_vector_type(4)));
+typedef float nt_v4f __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int4 load_nt(const int32_t* p) {
+  const nt_v4i v = __builtin_nontemporal_load(reinterpret_cast<const nt_v4i*>(p));
+  return int4{v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ float4 load_nt(const float* p) {
+  const nt_v4f v = __builtin_nontemporal_load(reinterpret_cast<const nt_v4f*>(p));
+  return float4{v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ void store_nt(float* p, float4 v) {
+  __builtin_nontemporal_store(nt_v4f{v.x, v.y, v.z, v.w}, reinterpret_cast<nt_v4f*>(p));
+}
+
 __global__ __launch_bounds__(kThreads) void fill_u8(uint8_t* p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) p[i] = 0;
 }
@@ -136,12 +151,12 @@ __global__ __launch_bounds__(kThreads) void mark_blocks(const int32_t* __restric
   const int32_t body_end = head_end + ((e - head_end) & ~3);
   int32_t j = head_end + 4 * lane;
   if (j < body_end) {
-    int4 c = *reinterpret_cast<const int4*>(indices + j);
+    int4 c = load_nt(indices + j);
     while (true) {
       const int32_t jn = j + 256;
       const bool more = jn < body_end;
       int4 cn = c;
-      if (more) cn = *reinterpret_cast<const int4*>(indices + jn);
+      if (more) cn = load_nt(indices + jn);
       const int32_t k0 = c.x / kT, k1 = c.y / kT, k2 = c.z / kT, k3 = c.w / kT;
       row_flags[k0] = 1;
       if (k1 != k0) row_flags[k1] = 1;
@@ -320,7 +335,7 @@ __global__ __launch_bounds__(kThreads) void emit_blocks(Geometry g, const uint8_
       block_cols[pos] = bc;
       morton[pos] = (int64_t)(spread_even((uint32_t)br) | (spread_even((uint32_t)bc) << 1));
     }
-    reinterpret_cast<float4*>(values + pos * (kT * kT))[threadIdx.x] = float4{0.f, 0.f, 0.f, 0.f};
+    store_nt(values + pos * (kT * kT) + 4 * threadIdx.x, float4{0.f, 0.f, 0.f, 0.f});
   }
 }
 
@@ -343,10 +358,10 @@ __global__ __launch_bounds__(kThreads) void scatter_entries(const int32_t* __res
   for (int32_t j = b + lane; j < head_end; j += 64) put(indices[j], data[j]);
   const int32_t body_end = head_end + ((e - head_end) & ~3);
   for (int32_t j = head_end + 4 * lane; j < body_end; j += 256) {
-    const int4 c = *reinterpret_cast<const int4*>(indices + j);
-    const float4 v = *reinterpret_cast<const float4*>(data + j);
+    const int4 c = load_nt(indices + j);
+    const float4 v = load_nt(data + j);
     if ((c.x & 3) == 0 && c.w == c.x + 3) {
-      *reinterpret_cast<float4*>(values + (int64_t)row_rank[c.x / kT] * (kT * kT) + rr * kT + (c.x % kT)) = v;
+      store_nt(values + (int64_t)row_rank[c.x / kT] * (kT * kT) + rr * kT + (c.x % kT), v);
     } else {
       put(c.x, v.x);
       put(c.y, v.y);
