@@ -1,0 +1,117 @@
+"""HIP graph capture of the SpMM entry points.
+
+A serving loop records its launches in a HIP graph and replays them.  The
+library launches kernels only (no memset nodes), and once a plan, its
+row-major view and its split-row workspace exist, a call allocates nothing
+but its output.  So a replay must reproduce the eager result bit for bit.
+
+Each case warms up eagerly (which builds and caches the plan and view),
+captures one call on torch's capture stream (which gets its own split-row
+workspace, zeroed by a captured fill kernel), then replays the graph several
+times.  Between replays it clears the captured output, runs other eager SpMM
+work on the default stream and synchronises, and it checks every replay.  A
+final eager call checks that capturing left the cached state intact.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import cases
+import oracle
+import void_amd
+
+pytestmark = pytest.mark.gpu
+
+REPLAYS = 4
+
+
+def _bits(t):
+    if t.dtype in (torch.float32, torch.int32):
+        return t.view(torch.int32)
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16)
+    return t
+
+
+def _capture_and_check(fn, other):
+    ref = fn()
+    torch.cuda.synchronize()
+    ref = ref.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    torch.cuda.synchronize()
+    for _ in range(REPLAYS):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        other()
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(out), _bits(ref))
+    again = fn()
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(again), _bits(ref))
+    del g
+
+
+def _int8(case, dev):
+    q = void_amd.quantize_void_tensor(cases.make_void_tensor(case, "cpu")).to(dev)
+    bq, bs = oracle.quantize_i8_columns(case.b)
+    return q, torch.from_numpy(bq).to(dev), torch.from_numpy(bs).to(dev)
+
+
+def _other(dev):
+    """Eager SpMM work of its own, run between replays on the default stream."""
+    case = cases.uniform_blocks(512, 1024, 128, 120, seed=99)
+    q, bt, st = _int8(case, dev)
+    return lambda: void_amd.void_spmm_int8(q, bt, b_scale=st, epilogue="per_block", chunk_tiles=2)
+
+
+@pytest.mark.parametrize("epilogue", ["raw_i32", "row_mean", "per_block"])
+def test_graph_int8_one_round(gpu, epilogue):
+    """At most 512 workgroups and no split rows (the two-ring kernel)."""
+    case = cases.uniform_blocks(1024, 2048, 256, 300, seed=21)
+    q, bt, st = _int8(case, gpu)
+    _capture_and_check(lambda: void_amd.void_spmm_int8(q, bt, b_scale=st, epilogue=epilogue), _other(gpu))
+
+
+@pytest.mark.parametrize("epilogue", ["raw_i32", "row_mean", "per_block"])
+def test_graph_int8_split_rows(gpu, epilogue):
+    """Split rows: the fix-up's arrival counters must be back at zero after
+    every replay, or the next replay's reduction would go wrong."""
+    case = cases.uniform_blocks(1024, 2048, 256, 900, seed=3)
+    q, bt, st = _int8(case, gpu)
+    _capture_and_check(lambda: void_amd.void_spmm_int8(q, bt, b_scale=st, epilogue=epilogue, chunk_tiles=3),
+                       _other(gpu))
+
+
+def test_graph_int8_deep_grid(gpu):
+    """More than 512 workgroups without splits (the 3-tile ring)."""
+    case = cases.uniform_blocks(4096, 1024, 1024, 1500, seed=8)
+    q, bt, st = _int8(case, gpu)
+    _capture_and_check(lambda: void_amd.void_spmm_int8(q, bt, b_scale=st, epilogue="per_block"), _other(gpu))
+
+
+def test_graph_gelu_bf16_bias(gpu):
+    case = cases.uniform_blocks(512, 1024, 384, 200, seed=12)
+    q, bt, st = _int8(case, gpu)
+    bias = torch.from_numpy(np.random.default_rng(2).standard_normal(384).astype(np.float32)).to(gpu)
+    _capture_and_check(
+        lambda: void_amd.void_spmm_gelu(q, bt, bias=bias, b_scale=st, out_dtype=torch.bfloat16), _other(gpu))
+
+
+def test_graph_fp8(gpu):
+    case = cases.uniform_blocks(512, 1024, 256, 250, seed=13)
+    f8 = void_amd.void_tensor_to_fp8(cases.make_void_tensor(case, "cpu")).to(gpu)
+    bq, bs = oracle.quantize_fp8_tensor(case.b)
+    bt = torch.from_numpy(bq).to(gpu).view(torch.float8_e4m3fn)
+    _capture_and_check(
+        lambda: void_amd.void_spmm_fp8(f8, bt, output_dtype=torch.bfloat16, b_scale=float(bs)), _other(gpu))
+
+
+def test_graph_float(gpu):
+    case = cases.uniform_blocks(512, 1024, 256, 150, seed=14)
+    vt = cases.make_void_tensor(case, "cpu").to(gpu)
+    b = torch.from_numpy(case.b).to(gpu)
+    _capture_and_check(lambda: void_amd.void_spmm(vt, b), _other(gpu))
