@@ -1,8 +1,9 @@
 """void_spmm_int8_noalloc through the C ABI: the allocation-free entry point
 gives the same bits as void_spmm_int8 with a caller's workspace, on plans
 that split rows (so its static scratch is used) and on plans that do not,
-on two calls in a row with the second smaller, and it rejects plans beyond
-its scratch with VOID_ERR_WORKSPACE."""
+on two calls in a row with the second smaller, and replayed from a HIP
+graph that captured only the library call; it rejects plans beyond its
+scratch with VOID_ERR_WORKSPACE."""
 
 from __future__ import annotations
 
@@ -28,12 +29,14 @@ def _setup(case, dev):
     return qd, torch.from_numpy(bq).to(dev), torch.from_numpy(bs).to(dev)
 
 
-def _noalloc(qd, b, bs, epilogue, chunk, out_dtype):
-    """One call of void_spmm_int8_noalloc on the current stream."""
+def _noalloc(qd, b, bs, epilogue, chunk, out_dtype, out=None):
+    """One call of void_spmm_int8_noalloc on the current stream (into out
+    when given, else into a new NaN-filled tensor)."""
     dbsr = qd.device_bsr()
     plan = dbsr.plan(chunk)
     M, N = qd.shape[0], b.shape[1]
-    out = torch.full((M, N), float("nan"), device=b.device).to(out_dtype)
+    if out is None:
+        out = torch.full((M, N), float("nan"), device=b.device).to(out_dtype)
     cplan = _lib.Plan(items=plan.items.data_ptr(), n_items=plan.n_items, n_split_tiles=plan.n_split_tiles,
                       n_slots=plan.n_slots, chunk_tiles=plan.chunk)
     dense = _lib.DenseArgs(b=b.data_ptr(), ldb=b.stride(0), b_col_major=0, N=N, b_scale=1.0,
@@ -78,6 +81,35 @@ def test_noalloc_unsplit_and_c4(gpu):
         ref = _with_workspace(qd, b, bs, _lib.EPI_PER_BLOCK, chunk)
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int32), ref.view(torch.int32))
+
+
+def test_noalloc_graph_replays(gpu):
+    """Captured alone in a HIP graph (plan, output and scratch set up
+    eagerly beforehand), the call replays to the same bits as
+    void_spmm_int8 with a workspace, with the output cleared, other eager
+    work and a synchronisation between replays."""
+    case = cases.uniform_blocks(1024, 2048, 256, 900, seed=3)
+    other = cases.uniform_blocks(512, 1024, 128, 120, seed=99)
+    qd, b, bs = _setup(case, gpu)
+    qo, bo, so = _setup(other, gpu)
+    chunk = 3
+    ref = _with_workspace(qd, b, bs, _lib.EPI_PER_BLOCK, chunk)
+    out = torch.empty(case.M, case.N, device=gpu)
+    _noalloc(qd, b, bs, _lib.EPI_PER_BLOCK, chunk, torch.float32, out=out)  # eager: plan and scratch ready
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int32), ref.view(torch.int32))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _noalloc(qd, b, bs, _lib.EPI_PER_BLOCK, chunk, torch.float32, out=out)
+    for rep in range(4):
+        print(f"noalloc graph replay {rep}", flush=True)
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        _noalloc(qo, bo, so, _lib.EPI_PER_BLOCK, 2, torch.float32)  # eager use of the same scratch, ordered after
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), ref.view(torch.int32))
+    del g
 
 
 def test_noalloc_rejects_oversize_plan(gpu):
