@@ -74,3 +74,33 @@ def test_device_format_feeds_the_spmm(gpu):
     q_dev = void_amd.quantize_void_tensor(vt_dev)
     q_host = void_amd.quantize_void_tensor(void_amd.csr_to_void(A))
     assert torch.equal(q_dev.values.cpu(), q_host.values) and torch.equal(q_dev.scales.cpu(), q_host.scales)
+
+
+@pytest.mark.parametrize("M,K", [(1024, 2048), (1000, 1000)])
+def test_device_csr_full_blocks_and_holes(gpu, M, K):
+    """Dense blocks, and blocks with one element or one row missing or cut
+    by the matrix edge: every element the CSR does not store comes out
+    zero, even when the tile memory held NaNs before the conversion."""
+    case = cases.uniform_blocks(M, K, 32, 160, seed=17)
+    dense = oracle.densify(case.tiles, case.block_rows, case.block_cols, (M, K))
+    rng = np.random.default_rng(5)
+    nbr, nbc = -(-M // 32), -(-K // 32)
+    for t in rng.choice(len(case.block_rows), 40, replace=False):
+        r0, c0 = case.block_rows[t] * 32, case.block_cols[t] * 32
+        kind = t % 4
+        if kind == 0:
+            dense[r0 + rng.integers(0, min(32, M - r0)), c0] = 0.0            # first column of a segment
+        elif kind == 1:
+            dense[r0 + rng.integers(0, min(32, M - r0)), min(c0 + 31, K - 1)] = 0.0  # last column
+        elif kind == 2:
+            dense[r0 + rng.integers(0, min(32, M - r0)), c0 + rng.integers(1, min(31, K - c0))] = 0.0
+        else:
+            dense[r0 + rng.integers(0, min(32, M - r0)), c0:c0 + 32] = 0.0   # a whole row of the block
+    A = sp.csr_matrix(dense)
+    A.sort_indices()
+    host = void_amd.csr_to_void(A)
+    # Leave NaNs in freed memory of the tile array's size for the caching
+    # allocator to hand back to the conversion.
+    junk = torch.full((host.n_blocks, 32, 32), float("nan"), device=gpu)
+    del junk
+    _same(void_amd.csr_to_void(A, device="cuda"), host)
