@@ -19,7 +19,7 @@ U = 2.0 ** -24
 
 @pytest.mark.parametrize("grouped", [False, True])
 @pytest.mark.parametrize("M,K,N,n,seed", [(1024, 2048, 512, 600, 0), (100, 70, 36, 6, 1), (64, 96, 130, 5, 2),
-                                          (256, 4096, 66, 300, 3)])
+                                          (256, 4096, 66, 300, 3), (96, 128, 1000, 12, 4)])
 def test_sddmm_tiles(gpu, M, K, N, n, seed, grouped):
     # grouped: void_sddmm_rows_f32 (tiles of a block-row share their grad_c
     # rows; the last shape has rows of up to 128 tiles, i.e. many groups per
