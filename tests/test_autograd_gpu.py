@@ -17,14 +17,20 @@ pytestmark = pytest.mark.gpu
 U = 2.0 ** -24
 
 
-@pytest.mark.parametrize("grouped", [False, True])
+@pytest.mark.parametrize("grouped", [None, "ring", "rows"])
 @pytest.mark.parametrize("M,K,N,n,seed", [(1024, 2048, 512, 600, 0), (100, 70, 36, 6, 1), (64, 96, 130, 5, 2),
-                                          (256, 4096, 66, 300, 3), (96, 128, 1000, 12, 4)])
-def test_sddmm_tiles(gpu, M, K, N, n, seed, grouped):
+                                          (256, 4096, 66, 300, 3), (96, 128, 1000, 12, 4), (70, 1000, 20, 40, 5),
+                                          (500, 300, 8, 30, 6)])
+def test_sddmm_tiles(gpu, M, K, N, n, seed, grouped, monkeypatch):
     # grouped: void_sddmm_rows_f32 (tiles of a block-row share their grad_c
-    # rows; the last shape has rows of up to 128 tiles, i.e. many groups per
-    # row); otherwise void_sddmm_f32, one tile per workgroup.
+    # rows; the fourth shape has rows of up to 128 tiles, i.e. many groups
+    # per row), on its LDS-DMA ring where the operands allow (N a multiple
+    # of 4: chunks of 16 columns, the last one cut by N in the last three
+    # shapes) or forced onto the register-staged kernel ("rows"); otherwise
+    # void_sddmm_f32, one tile per workgroup.
     from void_amd.format import build_bsr_layout
+    if grouped == "rows":
+        monkeypatch.setenv("VOID_AMD_SDDMM", "rows")
     rng = np.random.default_rng(seed)
     nbr, nbc = -(-M // 32), -(-K // 32)
     flat = rng.choice(nbr * nbc, min(n, nbr * nbc), replace=False)

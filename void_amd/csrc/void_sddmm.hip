@@ -18,9 +18,13 @@
 
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cstdint>
+#include <cstdlib>
+#include <cstring>
 
 #include "void_amd.h"
+#include "lds_dma.h"
 
 extern "C" __attribute__((visibility("hidden"))) int void_internal_fail(int code, const char* msg);
 
@@ -262,12 +266,145 @@ __global__ __launch_bounds__(64 * kGW) void sddmm_rows_kernel(
   }
 }
 
+// Row-grouped SDDMM on an LDS-DMA ring (void_sddmm_rows_f32 with 16-byte
+// aligned operands).  One workgroup of 8 waves per group of up to 8 tiles of
+// one block-row, wave w on tile w, as above; the reduction over N runs in
+// chunks of 32 columns, double-buffered in LDS.  A stage holds the group's
+// dC block (32 rows x 32 columns, 4 KB) and each tile's B block (4 KB),
+// loaded by buffer_load ... lds: every wave issues exactly 5 loads per stage
+// (the four 8-row parts of its tile's B block and one part of dC, or a
+// dummy load at kOutOfRange for waves 4-7), so the waits are fixed vmcnt
+// counts.  Rows are 128 bytes; the 16-byte segment s of row r sits at
+// position s ^ (r & 7), so that the 8 rows an 8-lane read phase touches fall
+// on distinct banks.  Lane (i, g) reads row i, columns 16 g .. 16 g + 15 of
+// both blocks (four 16-byte LDS reads each) and MFMA s takes column
+// 16 g + s from both operands.  Two 72 KB workgroups per CU move 72 KB per
+// chunk for 4096 cycles of MFMA per SIMD, below the L2 -> LDS rate, so the
+// matrix cores bound the loop.  Against 16-column chunks in rings of 3 or 4
+// stages, and 32-column chunks in 3 stages (one workgroup per CU), this
+// shape measured fastest on c2, c3 and c5.
+constexpr int kRW = 8;                      // waves = tiles per group
+constexpr int kCW = 32;                     // columns of N per chunk
+constexpr int kRing = 2;                    // stages (double buffer)
+constexpr int kSegs = kCW / 4;              // 16-byte segments per block row
+constexpr int kRowsPerLoad = 64 / kSegs;    // block rows per 1 KB load
+constexpr int kLoadsPerBlk = kT / kRowsPerLoad;
+constexpr int kBlk = kT * kCW * 4;          // one 32 x kCW fp32 block
+constexpr int kStage = (1 + kRW) * kBlk;    // dC block, then one B block per wave
+constexpr int kRingJunk = kRing * kStage;   // 1 KB that the dummy loads fill
+constexpr int kRingSmem = kRingJunk + 1024;
+constexpr int kLoadsPerStage = kLoadsPerBlk + 1;  // per wave: its B block and one dC load (or a dummy)
+static_assert(kLoadsPerBlk <= kRW, "the dC block's loads go one per wave");
+static_assert(kRing >= 2 && kRing <= 4, "stage waits cover up to two stages ahead");
+
+// Swizzle of block row r: segment s at position s ^ swz(r), so that the 8
+// rows of an 8-lane read phase fall on distinct banks.
+__device__ __forceinline__ int swz(int r) { return kSegs == 8 ? (r & 7) : ((r >> 1) & 3); }
+
+template <int OUT>
+__global__ __launch_bounds__(64 * kRW) void sddmm_ring_kernel(
+    const float* __restrict__ dC, int64_t ldg, const float* __restrict__ B, int64_t ldb,
+    const int32_t* __restrict__ groups, const int32_t* __restrict__ col_idx, const int64_t* __restrict__ tile_index,
+    int32_t M, int32_t N, int32_t K, void* __restrict__ grad) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kRingSmem];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i = lane & 31, g = lane >> 5;
+  const int br = groups[3 * blockIdx.x], pos0 = groups[3 * blockIdx.x + 1], cnt = groups[3 * blockIdx.x + 2];
+  const bool has = wave < cnt;
+  const int bc = has ? col_idx[pos0 + wave] : 0;
+  const int64_t out_t = has ? (tile_index ? tile_index[pos0 + wave] : (int64_t)(pos0 + wave)) : 0;
+  const int n_chunks = (N + kCW - 1) / kCW;
+
+  // Load lane l of part h: row kRowsPerLoad h + l / kSegs, LDS position
+  // l % kSegs holding source segment (l % kSegs) ^ swz(row).  Rows past M
+  // (dC) or K (B), and segments past N (N is a multiple of 4 here), read
+  // zeros.
+  const v4s rx = sgpr_rsrc(dC + (int64_t)br * kT * ldg), ry = sgpr_rsrc(B + (int64_t)bc * kT * ldb);
+  int vy[kLoadsPerBlk], sy[kLoadsPerBlk];
+#pragma unroll
+  for (int h = 0; h < kLoadsPerBlk; ++h) {
+    const int row = kRowsPerLoad * h + lane / kSegs;
+    sy[h] = (lane % kSegs) ^ swz(row);
+    vy[h] = has && bc * kT + row < K ? row * (int)ldb * 4 + sy[h] * 16 : kOutOfRange;
+  }
+  // This wave's dC load (waves below kLoadsPerBlk): part `wave` of the block.
+  const bool x_wave = wave < kLoadsPerBlk;
+  const int xrow = kRowsPerLoad * (wave % kLoadsPerBlk) + lane / kSegs;
+  const int sxs = (lane % kSegs) ^ swz(xrow);
+  const int vx = x_wave && br * kT + xrow < M ? xrow * (int)ldg * 4 + sxs * 16 : kOutOfRange;
+  auto issue = [&](int ch) {
+    uint8_t* st = smem + (ch % kRing) * kStage;
+    const int n0 = ch * kCW;
+#pragma unroll
+    for (int h = 0; h < kLoadsPerBlk; ++h)
+      dma_b128(ry, st + (1 + wave) * kBlk + h * 1024, n0 + 4 * sy[h] < N ? vy[h] : kOutOfRange, n0 * 4);
+    dma_b128(rx, x_wave ? st + wave * 1024 : smem + kRingJunk, n0 + 4 * sxs < N ? vx : kOutOfRange, n0 * 4);
+  };
+
+  // Lane (i, g): row i, source segments kSegs / 2 g .. + kSegs / 2 - 1.
+  constexpr int kHalf = kSegs / 2;
+  int rd[kHalf];
+#pragma unroll
+  for (int q = 0; q < kHalf; ++q) rd[q] = i * (kCW * 4) + (((kHalf * g + q) ^ swz(i)) << 4);
+  v16f acc = {};
+#pragma unroll
+  for (int k = 0; k < kRing - 1; ++k)
+    if (k < n_chunks) issue(k);
+  for (int ch = 0; ch < n_chunks; ++ch) {
+    wait_stages<kLoadsPerStage>(min(n_chunks - 1, ch + kRing - 2) - ch);
+    // Every wave's part of chunk ch has landed, and every wave has finished
+    // reading chunk ch - 1, whose slot the next issue overwrites.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (ch + kRing - 1 < n_chunks) issue(ch + kRing - 1);
+    if (has) {
+      const uint8_t* st = smem + (ch % kRing) * kStage;
+      const uint8_t* yb = st + (1 + wave) * kBlk;
+      v4f x[kHalf], y[kHalf];
+#pragma unroll
+      for (int q = 0; q < kHalf; ++q) {
+        x[q] = *reinterpret_cast<const v4f*>(st + rd[q]);
+        y[q] = *reinterpret_cast<const v4f*>(yb + rd[q]);
+      }
+#pragma unroll
+      for (int q = 0; q < kHalf; ++q)
+#pragma unroll
+        for (int s2 = 0; s2 < 4; ++s2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x[q][s2], y[q][s2], acc, 0, 0, 0);
+    }
+  }
+  if (!has) return;
+  // Lane (j, g), register r: tile row 8 (r / 4) + 4 g + r % 4, column j.
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = 8 * (r >> 2) + 4 * g + (r & 3);
+    const int64_t off = out_t * (kT * kT) + row * kT + i;
+    const float v = acc[r];
+    if constexpr (OUT == VOID_DT_F32) static_cast<float*>(grad)[off] = v;
+    else if constexpr (OUT == VOID_DT_BF16) static_cast<uint16_t*>(grad)[off] = (uint16_t)bf16_bits(v);
+    else {
+      _Float16 h = (_Float16)v;
+      uint16_t u;
+      __builtin_memcpy(&u, &h, 2);
+      static_cast<uint16_t*>(grad)[off] = u;
+    }
+  }
+}
+
 template <int OUT, bool VEC>
 int go_rows(const float* dC, int64_t ldg, const float* B, int64_t ldb, const int32_t* groups, int32_t n_groups,
             const int32_t* col_idx, const int64_t* tile_index, int32_t M, int32_t N, int32_t K, void* grad,
             hipStream_t stream) {
-  hipLaunchKernelGGL((sddmm_rows_kernel<OUT, VEC>), dim3(n_groups), dim3(64 * kGW), 0, stream, dC, ldg, B, ldb,
-                     groups, col_idx, tile_index, M, N, K, grad);
+  // The ring kernel needs 16-byte rows and 31-bit offsets within 32 rows of
+  // either operand; VOID_AMD_SDDMM=rows keeps the register-staged kernel.
+  const char* force = getenv("VOID_AMD_SDDMM");
+  const bool ring = VEC && !(force && strcmp(force, "rows") == 0) && (int64_t)kT * ldg * 4 < INT32_MAX &&
+                    (int64_t)kT * ldb * 4 < INT32_MAX;
+  if (ring)
+    hipLaunchKernelGGL((sddmm_ring_kernel<OUT>), dim3(n_groups), dim3(64 * kRW), 0, stream, dC, ldg, B, ldb, groups,
+                       col_idx, tile_index, M, N, K, grad);
+  else
+    hipLaunchKernelGGL((sddmm_rows_kernel<OUT, VEC>), dim3(n_groups), dim3(64 * kGW), 0, stream, dC, ldg, B, ldb,
+                       groups, col_idx, tile_index, M, N, K, grad);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return void_internal_fail(VOID_ERR_HIP, hipGetErrorString(e));
   return VOID_OK;

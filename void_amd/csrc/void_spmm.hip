@@ -42,6 +42,7 @@
 #include <vector>
 
 #include "void_amd.h"
+#include "lds_dma.h"
 
 extern "C" size_t void_workspace_bytes(int32_t n_split_tiles, int32_t n_slots, int32_t N);
 
@@ -937,11 +938,9 @@ static_assert(2 * kCgBatch <= kInline, "the first two batches' columns come from
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 
 // Raw buffers (stride 0) span 2^31 - 1 bytes; the host checks that every
-// operand's offsets fit in 31 bits.  A per-lane offset of kOutOfRange makes
-// a load return zeros without a memory request: slots past the end of an
-// item are filled that way, so that the number of issued loads (and so every
-// vmcnt wait) stays fixed.
-constexpr int kOutOfRange = (int)0x80000000u;
+// operand's offsets fit in 31 bits.  Slots past the end of an item are
+// filled by loads at kOutOfRange (zeros, no memory request), so that the
+// number of issued loads (and so every vmcnt wait) stays fixed.
 
 __device__ __forceinline__ Rsrc make_rsrc(const void* p) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, 0x7fffffff, 0x00020000);
@@ -1102,52 +1101,7 @@ static_assert(kDmaStages >= 2 && kDmaStages <= 4, "stage waits cover up to two s
 // all measured within noise of it on c2, c3 and c5).
 constexpr int kStoreStream = 2 | 16;
 
-// The loads are inline asm, invisible to the compiler's wait insertion: given
-// the builtin, it cannot tell the ring's slots apart and waits for every
-// outstanding LDS load (vmcnt(0)) before each LDS read, which drains the
-// ring.  Invisible loads only ever make the compiler's own vmcnt waits
-// stricter (they return in order), so its waits stay correct; the ring's
-// waits are explicit.  The descriptor is a raw buffer (stride 0, 2^31 - 1
-// bytes) as make_rsrc builds, held in SGPRs.
-typedef int v4s __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ v4s sgpr_rsrc(const void* p) {
-  const uint64_t a = (uint64_t)(uintptr_t)p;
-  return v4s{__builtin_amdgcn_readfirstlane((int)(uint32_t)a), __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)),
-             0x7fffffff, 0x00020000};
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
-}
-
-// 16 bytes per lane: lane l writes LDS bytes lds + 16 l .. + 15.  soff must be
-// wave-uniform (it is made an SGPR here).
-__device__ __forceinline__ void dma_b128(v4s r, const void* lds, int voff, int soff) {
-  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
-               :: "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff)), "{m0}"(lds_addr(lds)) : "memory");
-}
-
-// 4 bytes per lane: lane l writes LDS bytes lds + 4 l .. + 3.
-__device__ __forceinline__ void dma_b32(v4s r, const void* lds, int voff, int soff) {
-  asm volatile("buffer_load_dword %0, %1, %2 offen lds"
-               :: "v"(voff), "s"(r), "s"(__builtin_amdgcn_readfirstlane(soff)), "{m0}"(lds_addr(lds)) : "memory");
-}
-
-// s_waitcnt vmcnt(n), also a compiler barrier for memory accesses (the
-// builtin is not one: LDS reads could move above it).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
-}
-
-// Wait until at most `ahead` stages of C loads each are outstanding.
-template <int C>
-__device__ __forceinline__ void wait_stages(int ahead) {
-  if (ahead >= 2) wait_vm<2 * C>();
-  else if (ahead == 1) wait_vm<C>();
-  else wait_vm<0>();
-}
+// LDS-DMA loads, their SGPR descriptors and the ring's waits: lds_dma.h.
 
 template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false, int RT = kDmaTiles, int KS = 1>
 __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
