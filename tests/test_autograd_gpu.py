@@ -51,6 +51,41 @@ def test_sddmm_tiles(gpu, M, K, N, n, seed, grouped, monkeypatch):
         assert np.all(np.abs(got[t].cpu().numpy() - ref) <= bound + 1e-30), t
 
 
+
+# One rounding of the output type on top of the fp32 bound (p significand
+# bits: 8 for bf16, 11 for fp16, plus half of fp16's subnormal spacing).
+_HALF = {torch.bfloat16: (2.0 ** -8, 0.0), torch.float16: (2.0 ** -11, 2.0 ** -25)}
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("grouped", [None, "ring", "rows"])
+def test_sddmm_tiles_half_outputs(gpu, out_dtype, grouped, monkeypatch):
+    """The gradient tiles of a half-precision VOIDTensor come out in its
+    dtype (autograd.py passes a_values.dtype): each kernel's bf16 and fp16
+    stores."""
+    from void_amd.format import build_bsr_layout
+    if grouped == "rows":
+        monkeypatch.setenv("VOID_AMD_SDDMM", "rows")
+    M, K, N = 640, 1024, 200
+    rng = np.random.default_rng(7)
+    nbr, nbc = M // 32, K // 32
+    flat = rng.choice(nbr * nbc, 150, replace=False)
+    rows, cols = (flat // nbc).astype(np.int32), (flat % nbc).astype(np.int32)
+    G = rng.standard_normal((M, N)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    tr, tc = torch.from_numpy(rows).to(gpu), torch.from_numpy(cols).to(gpu)
+    lay = build_bsr_layout(tr, tc, nbr, nbc, gpu) if grouped else None
+    got = _runtime.sddmm_tiles(torch.from_numpy(G).to(gpu), torch.from_numpy(B).to(gpu), tr, tc, (M, K),
+                               out_dtype, layout=lay)
+    assert got.dtype == out_dtype
+    rel, ab = _HALF[out_dtype]
+    G64, B64 = G.astype(np.float64), B.astype(np.float64)
+    for t in range(len(rows)):
+        x, y = G64[rows[t] * 32:(rows[t] + 1) * 32], B64[cols[t] * 32:(cols[t] + 1) * 32]
+        ref = x @ y.T
+        bound = N * U * (np.abs(x) @ np.abs(y).T) * (1 + rel) + rel * np.abs(ref) + ab
+        assert np.all(np.abs(got[t].float().cpu().numpy() - ref) <= bound + 1e-30), t
+
 def test_voidspmm_gradients(gpu):
     case = cases.uniform_blocks(512, 1024, 96, 150, seed=5)
     vt = cases.make_void_tensor(case, "cpu").to(gpu)
