@@ -17,20 +17,24 @@ pytestmark = pytest.mark.gpu
 U = 2.0 ** -24
 
 
-@pytest.mark.parametrize("grouped", [None, "ring", "rows"])
+@pytest.mark.parametrize("grouped", [None, "tile_rows", "ring", "rows"])
 @pytest.mark.parametrize("M,K,N,n,seed", [(1024, 2048, 512, 600, 0), (100, 70, 36, 6, 1), (64, 96, 130, 5, 2),
                                           (256, 4096, 66, 300, 3), (96, 128, 1000, 12, 4), (70, 1000, 20, 40, 5),
                                           (500, 300, 8, 30, 6)])
 def test_sddmm_tiles(gpu, M, K, N, n, seed, grouped, monkeypatch):
-    # grouped: void_sddmm_rows_f32 (tiles of a block-row share their grad_c
-    # rows; the fourth shape has rows of up to 128 tiles, i.e. many groups
-    # per row), on its LDS-DMA ring where the operands allow (N a multiple
-    # of 4: chunks of 16 columns, the last one cut by N in the last three
-    # shapes) or forced onto the register-staged kernel ("rows"); otherwise
-    # void_sddmm_f32, one tile per workgroup.
+    # "ring" / "rows": void_sddmm_rows_f32 (tiles of a block-row share their
+    # grad_c rows; the fourth shape has rows of up to 128 tiles, i.e. many
+    # groups per row), on its LDS-DMA ring where the operands allow (N a
+    # multiple of 4: chunks of 32 columns, the last one cut by N in several
+    # shapes) or forced onto the register-staged kernel.  None /
+    # "tile_rows": void_sddmm_f32 (tiles in the given order, 8 to a
+    # workgroup on the per-tile ring with 16-column chunks, or one per
+    # workgroup on the register-staged kernel).
     from void_amd.format import build_bsr_layout
-    if grouped == "rows":
+    if grouped in ("rows", "tile_rows"):
         monkeypatch.setenv("VOID_AMD_SDDMM", "rows")
+    if grouped == "tile_rows":
+        grouped = None
     rng = np.random.default_rng(seed)
     nbr, nbc = -(-M // 32), -(-K // 32)
     flat = rng.choice(nbr * nbc, min(n, nbr * nbc), replace=False)
@@ -58,14 +62,16 @@ _HALF = {torch.bfloat16: (2.0 ** -8, 0.0), torch.float16: (2.0 ** -11, 2.0 ** -2
 
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
-@pytest.mark.parametrize("grouped", [None, "ring", "rows"])
+@pytest.mark.parametrize("grouped", [None, "tile_rows", "ring", "rows"])
 def test_sddmm_tiles_half_outputs(gpu, out_dtype, grouped, monkeypatch):
     """The gradient tiles of a half-precision VOIDTensor come out in its
     dtype (autograd.py passes a_values.dtype): each kernel's bf16 and fp16
     stores."""
     from void_amd.format import build_bsr_layout
-    if grouped == "rows":
+    if grouped in ("rows", "tile_rows"):
         monkeypatch.setenv("VOID_AMD_SDDMM", "rows")
+    if grouped == "tile_rows":
+        grouped = None
     M, K, N = 640, 1024, 200
     rng = np.random.default_rng(7)
     nbr, nbc = M // 32, K // 32

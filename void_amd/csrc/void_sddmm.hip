@@ -283,70 +283,107 @@ __global__ __launch_bounds__(64 * kGW) void sddmm_rows_kernel(
 // matrix cores bound the loop.  Against 16-column chunks in rings of 3 or 4
 // stages, and 32-column chunks in 3 stages (one workgroup per CU), this
 // shape measured fastest on c2, c3 and c5.
-constexpr int kRW = 8;                      // waves = tiles per group
-constexpr int kCW = 32;                     // columns of N per chunk
-constexpr int kRing = 2;                    // stages (double buffer)
-constexpr int kSegs = kCW / 4;              // 16-byte segments per block row
-constexpr int kRowsPerLoad = 64 / kSegs;    // block rows per 1 KB load
-constexpr int kLoadsPerBlk = kT / kRowsPerLoad;
-constexpr int kBlk = kT * kCW * 4;          // one 32 x kCW fp32 block
-constexpr int kStage = (1 + kRW) * kBlk;    // dC block, then one B block per wave
-constexpr int kRingJunk = kRing * kStage;   // 1 KB that the dummy loads fill
-constexpr int kRingSmem = kRingJunk + 1024;
-constexpr int kLoadsPerStage = kLoadsPerBlk + 1;  // per wave: its B block and one dC load (or a dummy)
-static_assert(kLoadsPerBlk <= kRW, "the dC block's loads go one per wave");
-static_assert(kRing >= 2 && kRing <= 4, "stage waits cover up to two stages ahead");
+constexpr int kRW = 8;    // waves per workgroup, one tile each
+constexpr int kRing = 2;  // stages (double buffer)
 
-// Swizzle of block row r: segment s at position s ^ swz(r), so that the 8
-// rows of an 8-lane read phase fall on distinct banks.
-__device__ __forceinline__ int swz(int r) { return kSegs == 8 ? (r & 7) : ((r >> 1) & 3); }
+// Block geometry of a ring with CW columns of N per chunk: 16-byte segments
+// per block row, rows per 1 KB load, loads per 32-row block, block bytes.
+template <int CW>
+struct RingGeo {
+  static constexpr int kSegs = CW / 4;
+  static constexpr int kRowsPerLoad = 64 / kSegs;
+  static constexpr int kLoadsPerBlk = kT / kRowsPerLoad;
+  static constexpr int kBlk = kT * CW * 4;
+  // Segment s of block row r sits at position s ^ swz(r), so that the 8 rows
+  // of an 8-lane read phase fall on distinct banks.
+  __device__ static __forceinline__ int swz(int r) { return kSegs == 8 ? (r & 7) : ((r >> 1) & 3); }
+};
 
-template <int OUT>
+// PER_TILE (void_sddmm_f32, tiles in any order): wave w takes tile 8 b + w
+// of workgroup b with a dC block of its own; a stage holds each wave's dC
+// and B blocks of a 16-column chunk (32 KB, 64 KB double-buffered, two
+// workgroups per CU), 4 loads per wave.
+template <int OUT, bool PER_TILE>
 __global__ __launch_bounds__(64 * kRW) void sddmm_ring_kernel(
     const float* __restrict__ dC, int64_t ldg, const float* __restrict__ B, int64_t ldb,
     const int32_t* __restrict__ groups, const int32_t* __restrict__ col_idx, const int64_t* __restrict__ tile_index,
+    const int32_t* __restrict__ block_rows, const int32_t* __restrict__ block_cols, int32_t n_blocks,
     int32_t M, int32_t N, int32_t K, void* __restrict__ grad) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kRingSmem];
+  constexpr int kCW = PER_TILE ? 16 : 32;  // columns of N per chunk
+  using Geo = RingGeo<kCW>;
+  constexpr int kSegs = Geo::kSegs, kRowsPerLoad = Geo::kRowsPerLoad, kLoadsPerBlk = Geo::kLoadsPerBlk;
+  constexpr int kBlk = Geo::kBlk;
+  constexpr int kStage = PER_TILE ? 2 * kRW * kBlk : (1 + kRW) * kBlk;
+  constexpr int kRingJunk = kRing * kStage;  // 1 KB that the dummy dC loads fill
+  constexpr int kLoadsPerStage = PER_TILE ? 2 * kLoadsPerBlk : kLoadsPerBlk + 1;
+  static_assert(kLoadsPerBlk <= kRW, "the shared dC block's loads go one per wave");
+  static_assert(kRing >= 2 && kRing <= 4, "stage waits cover up to two stages ahead");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kRingJunk + 1024];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i = lane & 31, g = lane >> 5;
-  const int br = groups[3 * blockIdx.x], pos0 = groups[3 * blockIdx.x + 1], cnt = groups[3 * blockIdx.x + 2];
-  const bool has = wave < cnt;
-  const int bc = has ? col_idx[pos0 + wave] : 0;
-  const int64_t out_t = has ? (tile_index ? tile_index[pos0 + wave] : (int64_t)(pos0 + wave)) : 0;
+  bool has;
+  int br, bc;
+  int64_t out_t;
+  if constexpr (PER_TILE) {
+    const int64_t t = (int64_t)blockIdx.x * kRW + wave;
+    has = t < n_blocks;
+    br = has ? block_rows[t] : 0;
+    bc = has ? block_cols[t] : 0;
+    out_t = t;
+  } else {
+    br = groups[3 * blockIdx.x];
+    const int pos0 = groups[3 * blockIdx.x + 1], cnt = groups[3 * blockIdx.x + 2];
+    has = wave < cnt;
+    bc = has ? col_idx[pos0 + wave] : 0;
+    out_t = has ? (tile_index ? tile_index[pos0 + wave] : (int64_t)(pos0 + wave)) : 0;
+  }
   const int n_chunks = (N + kCW - 1) / kCW;
+  // This wave's blocks within a stage.
+  const int xoff = PER_TILE ? 2 * wave * kBlk : 0;
+  const int yoff = PER_TILE ? (2 * wave + 1) * kBlk : (1 + wave) * kBlk;
 
   // Load lane l of part h: row kRowsPerLoad h + l / kSegs, LDS position
   // l % kSegs holding source segment (l % kSegs) ^ swz(row).  Rows past M
   // (dC) or K (B), and segments past N (N is a multiple of 4 here), read
   // zeros.
   const v4s rx = sgpr_rsrc(dC + (int64_t)br * kT * ldg), ry = sgpr_rsrc(B + (int64_t)bc * kT * ldb);
-  int vy[kLoadsPerBlk], sy[kLoadsPerBlk];
+  int vy[kLoadsPerBlk], vx[kLoadsPerBlk], sg[kLoadsPerBlk];
 #pragma unroll
   for (int h = 0; h < kLoadsPerBlk; ++h) {
+    // Grouped: wave w loads only part w of the shared dC block.
+    const int hx = PER_TILE ? h : wave % kLoadsPerBlk;
     const int row = kRowsPerLoad * h + lane / kSegs;
-    sy[h] = (lane % kSegs) ^ swz(row);
-    vy[h] = has && bc * kT + row < K ? row * (int)ldb * 4 + sy[h] * 16 : kOutOfRange;
+    const int xrow = kRowsPerLoad * hx + lane / kSegs;
+    sg[h] = (lane % kSegs) ^ Geo::swz(row);
+    vy[h] = has && bc * kT + row < K ? row * (int)ldb * 4 + sg[h] * 16 : kOutOfRange;
+    const bool x_live = PER_TILE ? has : wave < kLoadsPerBlk;
+    vx[h] = x_live && br * kT + xrow < M ? xrow * (int)ldg * 4 + ((lane % kSegs) ^ Geo::swz(xrow)) * 16 : kOutOfRange;
   }
-  // This wave's dC load (waves below kLoadsPerBlk): part `wave` of the block.
-  const bool x_wave = wave < kLoadsPerBlk;
-  const int xrow = kRowsPerLoad * (wave % kLoadsPerBlk) + lane / kSegs;
-  const int sxs = (lane % kSegs) ^ swz(xrow);
-  const int vx = x_wave && br * kT + xrow < M ? xrow * (int)ldg * 4 + sxs * 16 : kOutOfRange;
   auto issue = [&](int ch) {
     uint8_t* st = smem + (ch % kRing) * kStage;
     const int n0 = ch * kCW;
 #pragma unroll
     for (int h = 0; h < kLoadsPerBlk; ++h)
-      dma_b128(ry, st + (1 + wave) * kBlk + h * 1024, n0 + 4 * sy[h] < N ? vy[h] : kOutOfRange, n0 * 4);
-    dma_b128(rx, x_wave ? st + wave * 1024 : smem + kRingJunk, n0 + 4 * sxs < N ? vx : kOutOfRange, n0 * 4);
+      dma_b128(ry, st + yoff + h * 1024, n0 + 4 * sg[h] < N ? vy[h] : kOutOfRange, n0 * 4);
+    if constexpr (PER_TILE) {
+#pragma unroll
+      for (int h = 0; h < kLoadsPerBlk; ++h)
+        dma_b128(rx, st + xoff + h * 1024, n0 + 4 * sg[h] < N ? vx[h] : kOutOfRange, n0 * 4);
+    } else {
+      // The dC part's rows lie whole 8-row groups from part 0's, and with 8
+      // segments per row the swizzle depends only on the row mod 8, so
+      // sg[0] is this lane's dC segment too.
+      const bool x_wave = wave < kLoadsPerBlk;
+      dma_b128(rx, x_wave ? st + wave * 1024 : smem + kRingJunk, n0 + 4 * sg[0] < N ? vx[0] : kOutOfRange, n0 * 4);
+    }
   };
 
   // Lane (i, g): row i, source segments kSegs / 2 g .. + kSegs / 2 - 1.
   constexpr int kHalf = kSegs / 2;
   int rd[kHalf];
 #pragma unroll
-  for (int q = 0; q < kHalf; ++q) rd[q] = i * (kCW * 4) + (((kHalf * g + q) ^ swz(i)) << 4);
+  for (int q = 0; q < kHalf; ++q) rd[q] = i * (kCW * 4) + (((kHalf * g + q) ^ Geo::swz(i)) << 4);
   v16f acc = {};
 #pragma unroll
   for (int k = 0; k < kRing - 1; ++k)
@@ -359,12 +396,11 @@ __global__ __launch_bounds__(64 * kRW) void sddmm_ring_kernel(
     if (ch + kRing - 1 < n_chunks) issue(ch + kRing - 1);
     if (has) {
       const uint8_t* st = smem + (ch % kRing) * kStage;
-      const uint8_t* yb = st + (1 + wave) * kBlk;
       v4f x[kHalf], y[kHalf];
 #pragma unroll
       for (int q = 0; q < kHalf; ++q) {
-        x[q] = *reinterpret_cast<const v4f*>(st + rd[q]);
-        y[q] = *reinterpret_cast<const v4f*>(yb + rd[q]);
+        x[q] = *reinterpret_cast<const v4f*>(st + xoff + rd[q]);
+        y[q] = *reinterpret_cast<const v4f*>(st + yoff + rd[q]);
       }
 #pragma unroll
       for (int q = 0; q < kHalf; ++q)
@@ -390,18 +426,35 @@ __global__ __launch_bounds__(64 * kRW) void sddmm_ring_kernel(
   }
 }
 
+// The ring kernels need 16-byte rows (VEC) and 31-bit offsets within 32
+// rows of either operand; VOID_AMD_SDDMM=rows keeps the register-staged
+// kernels.
+bool use_ring(bool vec, int64_t ldg, int64_t ldb) {
+  const char* force = getenv("VOID_AMD_SDDMM");
+  return vec && !(force && strcmp(force, "rows") == 0) && (int64_t)kT * ldg * 4 < INT32_MAX &&
+         (int64_t)kT * ldb * 4 < INT32_MAX;
+}
+
+// void_sddmm_f32: the per-tile ring where the operands allow, else one
+// workgroup per tile on the register-staged kernel.
+template <int OUT, bool VEC>
+int go_tiles(const float* dC, int64_t ldg, const float* B, int64_t ldb, const int32_t* rows, const int32_t* cols,
+             int32_t n, int32_t M, int32_t N, int32_t K, void* grad, hipStream_t stream) {
+  if (!use_ring(VEC, ldg, ldb)) return go<OUT, VEC>(dC, ldg, B, ldb, rows, cols, n, M, N, K, grad, stream);
+  hipLaunchKernelGGL((sddmm_ring_kernel<OUT, true>), dim3((n + kRW - 1) / kRW), dim3(64 * kRW), 0, stream, dC, ldg, B,
+                     ldb, nullptr, nullptr, nullptr, rows, cols, n, M, N, K, grad);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return void_internal_fail(VOID_ERR_HIP, hipGetErrorString(e));
+  return VOID_OK;
+}
+
 template <int OUT, bool VEC>
 int go_rows(const float* dC, int64_t ldg, const float* B, int64_t ldb, const int32_t* groups, int32_t n_groups,
             const int32_t* col_idx, const int64_t* tile_index, int32_t M, int32_t N, int32_t K, void* grad,
             hipStream_t stream) {
-  // The ring kernel needs 16-byte rows and 31-bit offsets within 32 rows of
-  // either operand; VOID_AMD_SDDMM=rows keeps the register-staged kernel.
-  const char* force = getenv("VOID_AMD_SDDMM");
-  const bool ring = VEC && !(force && strcmp(force, "rows") == 0) && (int64_t)kT * ldg * 4 < INT32_MAX &&
-                    (int64_t)kT * ldb * 4 < INT32_MAX;
-  if (ring)
-    hipLaunchKernelGGL((sddmm_ring_kernel<OUT>), dim3(n_groups), dim3(64 * kRW), 0, stream, dC, ldg, B, ldb, groups,
-                       col_idx, tile_index, M, N, K, grad);
+  if (use_ring(VEC, ldg, ldb))
+    hipLaunchKernelGGL((sddmm_ring_kernel<OUT, false>), dim3(n_groups), dim3(64 * kRW), 0, stream, dC, ldg, B, ldb,
+                       groups, col_idx, tile_index, nullptr, nullptr, 0, M, N, K, grad);
   else
     hipLaunchKernelGGL((sddmm_rows_kernel<OUT, VEC>), dim3(n_groups), dim3(64 * kGW), 0, stream, dC, ldg, B, ldb,
                        groups, col_idx, tile_index, M, N, K, grad);
@@ -426,14 +479,14 @@ extern "C" int void_sddmm_f32(const float* grad_c, int64_t ldg, const float* b, 
                    N % 4 == 0;
   switch (out_dtype) {
     case VOID_DT_F32:
-      return vec ? go<VOID_DT_F32, true>(grad_c, ldg, b, ldb, block_rows, block_cols, n_blocks, M, N, K, grad_tiles, stream)
-                 : go<VOID_DT_F32, false>(grad_c, ldg, b, ldb, block_rows, block_cols, n_blocks, M, N, K, grad_tiles, stream);
+      return vec ? go_tiles<VOID_DT_F32, true>(grad_c, ldg, b, ldb, block_rows, block_cols, n_blocks, M, N, K, grad_tiles, stream)
+                 : go_tiles<VOID_DT_F32, false>(grad_c, ldg, b, ldb, block_rows, block_cols, n_blocks, M, N, K, grad_tiles, stream);
     case VOID_DT_BF16:
-      return vec ? go<VOID_DT_BF16, true>(grad_c, ldg, b, ldb, block_rows, block_cols, n_blocks, M, N, K, grad_tiles, stream)
-                 : go<VOID_DT_BF16, false>(grad_c, ldg, b, ldb, block_rows, block_cols, n_blocks, M, N, K, grad_tiles, stream);
+      return vec ? go_tiles<VOID_DT_BF16, true>(grad_c, ldg, b, ldb, block_rows, block_cols, n_blocks, M, N, K, grad_tiles, stream)
+                 : go_tiles<VOID_DT_BF16, false>(grad_c, ldg, b, ldb, block_rows, block_cols, n_blocks, M, N, K, grad_tiles, stream);
     case VOID_DT_F16:
-      return vec ? go<VOID_DT_F16, true>(grad_c, ldg, b, ldb, block_rows, block_cols, n_blocks, M, N, K, grad_tiles, stream)
-                 : go<VOID_DT_F16, false>(grad_c, ldg, b, ldb, block_rows, block_cols, n_blocks, M, N, K, grad_tiles, stream);
+      return vec ? go_tiles<VOID_DT_F16, true>(grad_c, ldg, b, ldb, block_rows, block_cols, n_blocks, M, N, K, grad_tiles, stream)
+                 : go_tiles<VOID_DT_F16, false>(grad_c, ldg, b, ldb, block_rows, block_cols, n_blocks, M, N, K, grad_tiles, stream);
     default:
       return void_internal_fail(VOID_ERR_UNSUPPORTED, "gradient tiles are f32, bf16 or f16");
   }
