@@ -170,17 +170,23 @@ __global__ __launch_bounds__(kThreads) void mark_blocks(const int32_t* __restric
   for (int32_t t = body_end + lane; t < e; t += 64) row_flags[indices[t] / kT] = 1;
 }
 
+// Even bits of a small x (below 64), packed: the row part of a low Morton
+// code; constant-folded where x is.
+__device__ __forceinline__ int even_bits6(int x) { return (x & 1) | ((x >> 1) & 2) | ((x >> 2) & 4); }
+
 // Flags of the P codes [c0, c0 + P) into bit i of the result, all loads issued
 // before any is used (codes outside the grid read flag 0 and count as 0).
+// c0 is a multiple of P (a power of two), so code c0 + i has the block row
+// and column of c0 plus those of i, which are constants once unrolled.
 template <int P>
 __device__ __forceinline__ uint32_t flag_bits(const uint8_t* flags, const Geometry& g, int64_t c0) {
-  static_assert(P <= 32, "one bit per code");
+  static_assert(P <= 32 && (P & (P - 1)) == 0, "one bit per code, aligned runs");
+  const int32_t br0 = (int32_t)compact_even((uint64_t)c0), bc0 = (int32_t)compact_even((uint64_t)c0 >> 1);
   uint8_t f[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) {
-    const int64_t c = c0 + i;
-    const int32_t br = (int32_t)compact_even((uint64_t)c), bc = (int32_t)compact_even((uint64_t)c >> 1);
-    const bool in = c < g.n_codes && br < g.n_br && bc < g.n_bc;
+    const int32_t br = br0 + even_bits6(i), bc = bc0 + even_bits6(i >> 1);
+    const bool in = c0 + i < g.n_codes && br < g.n_br && bc < g.n_bc;
     f[i] = flags[in ? (int64_t)br * g.n_bc + bc : 0] & (in ? 1 : 0);
   }
   uint32_t m = 0;
@@ -269,6 +275,7 @@ __global__ __launch_bounds__(kSmallThreads) void rank_small(Geometry g, const ui
   __syncthreads();
   const int64_t c0 = (int64_t)threadIdx.x * kSmallPer;
   const uint32_t bits = flag_bits<kSmallPer>(lflags, g, c0);
+  const int32_t br0 = (int32_t)compact_even((uint64_t)c0), bc0 = (int32_t)compact_even((uint64_t)c0 >> 1);
   const int n = __builtin_popcount(bits);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int v = n;
@@ -287,8 +294,8 @@ __global__ __launch_bounds__(kSmallThreads) void rank_small(Geometry g, const ui
   }
   int pos = base + v - n;
   for (uint32_t m = bits; m; m &= m - 1) {
-    const int64_t c = c0 + __builtin_ctz(m);
-    const int32_t br = (int32_t)compact_even((uint64_t)c), bc = (int32_t)compact_even((uint64_t)c >> 1);
+    const int k = __builtin_ctz(m);  // code c0 + k: c0's row and column plus k's
+    const int32_t br = br0 + even_bits6(k), bc = bc0 + even_bits6(k >> 1);
     rank[(int64_t)br * g.n_bc + bc] = pos++;
   }
   if (threadIdx.x == 0) {
@@ -305,12 +312,13 @@ __global__ __launch_bounds__(kThreads) void rank_blocks(Geometry g, const uint8_
   __shared__ int sh[kThreads / 64];
   const int64_t c0 = (int64_t)blockIdx.x * kChunk + (int64_t)threadIdx.x * kPerThread;
   const uint32_t bits = flag_bits<kPerThread>(flags, g, c0);
+  const int32_t br0 = (int32_t)compact_even((uint64_t)c0), bc0 = (int32_t)compact_even((uint64_t)c0 >> 1);
   const int n = __builtin_popcount(bits);
   const int incl = block_sum(n, sh);
   int64_t pos = chunk[blockIdx.x] + (incl - n);
   for (uint32_t m = bits; m; m &= m - 1) {
-    const int64_t c = c0 + __builtin_ctz(m);
-    const int32_t br = (int32_t)compact_even((uint64_t)c), bc = (int32_t)compact_even((uint64_t)c >> 1);
+    const int k = __builtin_ctz(m);  // code c0 + k: c0's row and column plus k's
+    const int32_t br = br0 + even_bits6(k), bc = bc0 + even_bits6(k >> 1);
     rank[(int64_t)br * g.n_bc + bc] = (int32_t)pos++;
   }
 }
