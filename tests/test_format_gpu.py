@@ -23,11 +23,13 @@ def _same(dev_vt, host_vt):
         assert torch.equal(a, b), name
 
 
-# Morton code spaces up to 32768 codes rank in one workgroup; the last two
-# shapes (65536 and 2^20 codes) take the chunked count / scan / rank path.
+# Morton code spaces up to 32768 codes rank in one workgroup; larger ones
+# count per chunk of 4096 codes and rank with the chunks' offsets, summed in
+# each workgroup up to 256 chunks (65536 and 2^20 codes here) and by a
+# separate scan beyond (2^22 codes, the last shape).
 @pytest.mark.parametrize("M,N,density,seed", [(300, 200, 0.05, 1), (2000, 70, 0.02, 2), (70, 3000, 0.02, 3),
                                               (4096, 4096, 0.002, 4), (33, 33, 0.5, 5), (1, 1000, 0.1, 6),
-                                              (8192, 6000, 0.0005, 7), (20000, 64, 0.01, 8)])
+                                              (8192, 6000, 0.0005, 7), (20000, 64, 0.01, 8), (33000, 40, 0.001, 9)])
 def test_device_csr_to_void_matches_host(gpu, M, N, density, seed):
     A = sp.random(M, N, density=density, format="csr", random_state=seed, dtype=np.float64)
     A.sort_indices()

@@ -305,17 +305,40 @@ __global__ __launch_bounds__(kSmallThreads) void rank_small(Geometry g, const ui
 }
 
 // 2''. Large code spaces: the Morton rank of every flagged block from the
-// scanned chunk counts.
+// chunk offsets.  LOCAL (at most kThreads chunks): chunk[] holds the counts,
+// each workgroup sums those of the chunks below its own, and the last one
+// writes the total, so no separate scan runs; otherwise chunk[] holds the
+// offsets from scan_chunks.
+template <bool LOCAL>
 __global__ __launch_bounds__(kThreads) void rank_blocks(Geometry g, const uint8_t* __restrict__ flags,
                                                         const int64_t* __restrict__ chunk,
-                                                        int32_t* __restrict__ rank) {
+                                                        int32_t* __restrict__ rank, int64_t* __restrict__ total,
+                                                        int64_t* __restrict__ count) {
   __shared__ int sh[kThreads / 64];
+  __shared__ int s_base;
   const int64_t c0 = (int64_t)blockIdx.x * kChunk + (int64_t)threadIdx.x * kPerThread;
   const uint32_t bits = flag_bits<kPerThread>(flags, g, c0);
   const int32_t br0 = (int32_t)compact_even((uint64_t)c0), bc0 = (int32_t)compact_even((uint64_t)c0 >> 1);
+  int64_t base;
+  if constexpr (LOCAL) {
+    // A chunk holds at most kChunk blocks, so the sums fit an int.
+    const int below = threadIdx.x < blockIdx.x ? (int)chunk[threadIdx.x] : 0;
+    const int b_incl = block_sum(below, sh);
+    if (threadIdx.x == kThreads - 1) s_base = b_incl;
+    __syncthreads();
+    base = s_base;
+  } else {
+    base = chunk[blockIdx.x];
+  }
   const int n = __builtin_popcount(bits);
   const int incl = block_sum(n, sh);
-  int64_t pos = chunk[blockIdx.x] + (incl - n);
+  if constexpr (LOCAL) {
+    if (blockIdx.x == gridDim.x - 1 && threadIdx.x == kThreads - 1) {
+      *total = base + incl;
+      *count = base + incl;
+    }
+  }
+  int64_t pos = base + (incl - n);
   for (uint32_t m = bits; m; m &= m - 1) {
     const int k = __builtin_ctz(m);  // code c0 + k: c0's row and column plus k's
     const int32_t br = br0 + even_bits6(k), bc = bc0 + even_bits6(k >> 1);
@@ -422,9 +445,14 @@ int void_csr_count_blocks(const int32_t* indptr, const int32_t* indices, int32_t
     hipLaunchKernelGGL(rank_small, dim3(1), dim3(kSmallThreads), 0, stream, g, w.flags, w.rank, w.total, n_blocks);
   } else {
     hipLaunchKernelGGL(count_chunks, dim3((unsigned)g.n_chunks), dim3(kThreads), 0, stream, g, w.flags, w.chunk);
-    hipLaunchKernelGGL(scan_chunks, dim3(1), dim3(kThreads), 0, stream, g.n_chunks, w.chunk, w.total, n_blocks);
-    hipLaunchKernelGGL(rank_blocks, dim3((unsigned)g.n_chunks), dim3(kThreads), 0, stream, g, w.flags, w.chunk,
-                       w.rank);
+    if (g.n_chunks <= kThreads) {
+      hipLaunchKernelGGL(rank_blocks<true>, dim3((unsigned)g.n_chunks), dim3(kThreads), 0, stream, g, w.flags,
+                         w.chunk, w.rank, w.total, n_blocks);
+    } else {
+      hipLaunchKernelGGL(scan_chunks, dim3(1), dim3(kThreads), 0, stream, g.n_chunks, w.chunk, w.total, n_blocks);
+      hipLaunchKernelGGL(rank_blocks<false>, dim3((unsigned)g.n_chunks), dim3(kThreads), 0, stream, g, w.flags,
+                         w.chunk, w.rank, nullptr, nullptr);
+    }
   }
   return launched();
 }
