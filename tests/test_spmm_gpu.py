@@ -388,3 +388,37 @@ def test_abi_empty_matrix_null_pointers(gpu, epilogue, kernel):
     assert st == 0, _lib.lib().void_last_error()
     torch.cuda.synchronize()
     assert torch.count_nonzero(out.nan_to_num(1.0)) == 0
+
+
+def test_inplace_updates_are_seen(gpu):
+    """The reference reads the tiles and scales on every call; the cached
+    block-row-major device copy is gathered again after they change in
+    place (values or scales of Int8VOIDTensor, values of a float
+    VOIDTensor, scales of an FP8VOIDTensor)."""
+    case = cases.uniform_blocks(256, 512, 128, 40, seed=21)
+    case2 = cases.BlockCase(case.name, case.M, case.K, case.N, (-0.37 * case.tiles[::-1]).copy(),
+                            case.block_rows, case.block_cols, case.b)
+    qd, A, bq, bs = _int8_setup(case, gpu)
+    bt, st = torch.from_numpy(bq).to(gpu), torch.from_numpy(bs).to(gpu)
+    first = void_amd.void_spmm_int8(qd, bt, b_scale=st, epilogue="raw_i32")
+    q2 = void_amd.quantize_void_tensor(cases.make_void_tensor(case2, "cpu")).to(gpu)
+    qd.values.copy_(q2.values)
+    qd.scales.copy_(q2.scales)
+    for epi in ("raw_i32", "per_block", "row_mean"):
+        got = void_amd.void_spmm_int8(qd, bt, b_scale=st, epilogue=epi)
+        ref = void_amd.void_spmm_int8(q2, bt, b_scale=st, epilogue=epi)
+        assert torch.equal(got.view(torch.int32), ref.view(torch.int32)), epi
+    assert not torch.equal(first, void_amd.void_spmm_int8(qd, bt, b_scale=st, epilogue="raw_i32"))
+
+    vt = cases.make_void_tensor(case, "cpu").to(gpu)
+    b32 = torch.from_numpy(case.b).to(gpu)
+    y1 = void_amd.void_spmm(vt, b32)
+    vt.values.mul_(0.5)  # a power of two: every product and sum scales exactly
+    assert torch.equal(void_amd.void_spmm(vt, b32), 0.5 * y1)
+
+    f8 = void_amd.void_tensor_to_fp8(cases.make_void_tensor(case, "cpu")).to(gpu)
+    b8q, b8s = oracle.quantize_fp8_tensor(case.b)
+    b8 = torch.from_numpy(b8q).to(gpu).view(torch.float8_e4m3fn)
+    z1 = void_amd.void_spmm_fp8(f8, b8, output_dtype=torch.float32, b_scale=float(b8s))
+    f8.scaling_info.scale.mul_(2.0)
+    assert torch.equal(void_amd.void_spmm_fp8(f8, b8, output_dtype=torch.float32, b_scale=float(b8s)), 2.0 * z1)

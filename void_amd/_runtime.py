@@ -37,6 +37,7 @@ class DevicePlan:
     chunk: int
     host_items: np.ndarray       # int32 [n_items, 32] copy, for inspection
     workspaces: Dict[Tuple[int, int], torch.Tensor] = field(default_factory=dict)
+    ws_sizes: Dict[int, int] = field(default_factory=dict)  # N -> void_workspace_bytes
 
     def workspace(self, N: int, device: torch.device,
                   stream: Optional[int] = None) -> Tuple[Optional[torch.Tensor], int]:
@@ -47,7 +48,9 @@ class DevicePlan:
         each stream gets its own (launches on one stream run in order, and
         every launch leaves the counters at zero).  ``stream`` is the raw
         stream handle, torch's current stream of ``device`` by default."""
-        nbytes = int(_lib.lib().void_workspace_bytes(self.n_split_tiles, self.n_slots, N))
+        nbytes = self.ws_sizes.get(N)
+        if nbytes is None:
+            nbytes = self.ws_sizes[N] = int(_lib.lib().void_workspace_bytes(self.n_split_tiles, self.n_slots, N))
         if nbytes == 0:
             return None, 0
         if stream is None:
@@ -213,12 +216,34 @@ class DeviceBsr:
     n_block_rows: int
     plans: Dict[int, DevicePlan] = field(default_factory=dict)
     _row_groups: Optional[RowGroupPlan] = None
+    _max_row: Optional[int] = None
+    _desc: Optional[_lib.BsrDesc] = None
+    order: Optional[torch.Tensor] = None  # BSR position -> index of the source tile
+    src_key: tuple = ()                   # source_key of the tensors the arrays were gathered from
+
+    def refresh(self, values: torch.Tensor, scales: torch.Tensor) -> None:
+        """Gather the tile values and scales again from their sources into the
+        existing arrays, after the sources changed in place; the block
+        structure, plans and descriptor stay valid."""
+        dev = self.tiles.device
+        v = values.to(dev)
+        if v.dtype != torch.uint8:
+            v = v.view(torch.uint8)
+        if self.n_blocks:
+            torch.index_select(v, 0, self.order, out=self.tiles)
+        sc = scales.to(device=dev, dtype=torch.float32)
+        if self.per_tensor:
+            self.scales.copy_(sc.reshape(-1)[:1])
+        elif sc.numel():
+            torch.index_select(sc, 0, self.order, out=self.scales)
 
     @property
     def max_row(self) -> int:
-        """Tiles in the longest block-row."""
-        rp = self.row_ptr_host
-        return int(np.max(np.diff(rp))) if len(rp) > 1 else 0
+        """Tiles in the longest block-row (the structure is fixed: computed once)."""
+        if self._max_row is None:
+            rp = self.row_ptr_host
+            self._max_row = int(np.max(np.diff(rp))) if len(rp) > 1 else 0
+        return self._max_row
 
     def plan(self, chunk: int) -> DevicePlan:
         p = self.plans.get(chunk)
@@ -259,6 +284,12 @@ class DeviceBsr:
         return tuning.use_row_groups(self.n_blocks, rg.n_steps, rg.n_groups, N, rg.max_stages)
 
     def desc(self) -> _lib.BsrDesc:
+        """The C descriptor of this matrix (its arrays never change: built once)."""
+        if self._desc is None:
+            self._desc = self._make_desc()
+        return self._desc
+
+    def _make_desc(self) -> _lib.BsrDesc:
         return _lib.BsrDesc(
             tiles=self.tiles.data_ptr() if self.n_blocks else None,
             scales=self.scales.data_ptr() if self.scales.numel() else None,
@@ -291,7 +322,15 @@ def make_device_bsr(values: torch.Tensor, scales: torch.Tensor, block_rows: torc
     return DeviceBsr(tiles=tiles, scales=s, row_ptr=lay.row_ptr, col_idx=lay.col_idx,
                      row_ptr_host=lay.row_ptr_host, col_idx_host=lay.col_idx.cpu().numpy(),
                      per_tensor=per_tensor, M=M, K=K,
-                     n_blocks=int(values.shape[0]), n_block_rows=n_br)
+                     n_blocks=int(values.shape[0]), n_block_rows=n_br, order=lay.order)
+
+
+def source_key(*tensors: torch.Tensor) -> tuple:
+    """Identity and in-place version of the tensors a device copy is made
+    from: the copy is stale once either changes.  Inference tensors
+    (torch.inference_mode) keep no version counter, so for them only a new
+    tensor is noticed."""
+    return tuple((t.data_ptr(), None if t.is_inference() else t._version) for t in tensors)
 
 
 def require_gpu(t: torch.Tensor, what: str) -> None:

@@ -126,15 +126,21 @@ class VOIDTensor:
 
     def device_bsr(self):
         """Block-row-major fp32 device copy of the tiles for the float kernel
-        (built once per device)."""
+        (built once per device, gathered again when the values change in
+        place, since the reference reads them on every call)."""
         from . import _runtime
         key = str(self.values.device)
+        src = _runtime.source_key(self.values)
         d = self._device_bsr.get(key)
         if d is None:
             ones = torch.ones(1, dtype=torch.float32, device=self.values.device)
             d = _runtime.make_device_bsr(self.values.to(torch.float32).contiguous(), ones, self.block_rows,
                                          self.block_cols, self.shape, self.tile_size, self.values.device, True)
+            d.src_key = src
             self._device_bsr[key] = d
+        elif d.src_key != src:
+            d.refresh(self.values.to(torch.float32).contiguous(), d.scales)
+            d.src_key = src
         return d
 
     @property

@@ -195,16 +195,23 @@ class FP8VOIDTensor:
                 + (self.block_rows.numel() + self.block_cols.numel()) * 4)
 
     def device_bsr(self) -> "_runtime.DeviceBsr":
+        """Block-row-major device copy of the tiles (built once per device,
+        gathered again when the codes or scales change in place)."""
         key = str(self.values_fp8.device)
+        scales = self.scaling_info.scale.reshape(-1)
+        src = _runtime.source_key(self.values_fp8, self.scaling_info.scale)
         d = self._device_bsr.get(key)
         if d is None:
             if self.values_fp8.dtype != torch.float8_e4m3fn:
                 raise NotImplementedError(f"the FP8 kernel takes E4M3FN tiles, got {self.values_fp8.dtype}")
             per_tensor = self.scaling_info.config.scale_mode == "per_tensor"
-            scales = self.scaling_info.scale.reshape(-1)
             d = _runtime.make_device_bsr(self.values_fp8, scales, self.block_rows, self.block_cols,
                                          self.shape, self.tile_size, self.values_fp8.device, per_tensor)
+            d.src_key = src
             self._device_bsr[key] = d
+        elif d.src_key != src:
+            d.refresh(self.values_fp8, scales)
+            d.src_key = src
         return d
 
     def __repr__(self) -> str:

@@ -128,9 +128,15 @@ class Int8VOIDTensor:
         return self._row_ptr, self._block_indices
 
     def device_bsr(self) -> "_runtime.DeviceBsr":
-        """Block-row-major device copy of the tiles (built once per device)."""
+        """Block-row-major device copy of the tiles (built once per device,
+        gathered again when the values or scales change in place, since the
+        reference reads them on every call)."""
         key = str(self.values.device)
+        src = _runtime.source_key(self.values, self.scales)
         d = self._device_bsr.get(key)
+        if d is not None and d.src_key != src:
+            d.refresh(self.values, self.scales)
+            d.src_key = src
         if d is None:
             if self.values.dtype != torch.int8:
                 raise NotImplementedError(
@@ -141,6 +147,7 @@ class Int8VOIDTensor:
             per_tensor = self.config.scale_mode == ScaleMode.PER_TENSOR
             d = _runtime.make_device_bsr(self.values, self.scales, self.block_rows, self.block_cols,
                                          self.shape, self.tile_size, self.values.device, per_tensor)
+            d.src_key = src
             self._device_bsr[key] = d
         return d
 
