@@ -133,3 +133,26 @@ def test_sparse_linear_training_step(gpu):
     W = oracle.densify(vt.values.cpu().numpy() * 2.0, case.block_rows, case.block_cols, (128, 256))
     ref = x.reshape(-1, 256).cpu().double().numpy() @ W.T.astype(np.float64)
     assert np.allclose(y2.detach().reshape(-1, 128).cpu().numpy(), ref, rtol=1e-5, atol=1e-4)
+
+
+
+def test_inference_mode(gpu):
+    """Tensors made under torch.inference_mode keep no version counter; the
+    cached layouts then key on identity alone, and every entry point runs as
+    outside that mode."""
+    case = cases.uniform_blocks(256, 512, 64, 40, seed=8)
+    x_host = torch.randn(512, 64)
+    vt_ref = cases.make_void_tensor(case, "cpu").to(gpu)
+    y_ref = void_amd.VOIDSpMM(vt_ref).to(gpu)(x_host.to(gpu)).detach()
+    q_ref = void_amd.quantize_void_tensor(cases.make_void_tensor(case, "cpu")).to(gpu)
+    bq, bs = oracle.quantize_i8_columns(case.b)
+    z_ref = void_amd.void_spmm_int8(q_ref, torch.from_numpy(bq).to(gpu), b_scale=torch.from_numpy(bs).to(gpu))
+    with torch.inference_mode():
+        vt = cases.make_void_tensor(case, "cpu").to(gpu)
+        mod = void_amd.VOIDSpMM(vt).to(gpu)
+        x = x_host.to(gpu)
+        assert torch.equal(mod(x), y_ref)
+        assert torch.equal(void_amd.void_spmm(vt, x), y_ref)
+        q = void_amd.quantize_void_tensor(cases.make_void_tensor(case, "cpu")).to(gpu)
+        z = void_amd.void_spmm_int8(q, torch.from_numpy(bq).to(gpu), b_scale=torch.from_numpy(bs).to(gpu))
+        assert torch.equal(z, z_ref)

@@ -25,16 +25,19 @@ _LAYOUTS: dict = {}
 
 
 def _layout(block_rows: torch.Tensor, block_cols: torch.Tensor, shape: Tuple[int, int]):
-    key = (block_rows.data_ptr(), block_cols.data_ptr(), int(block_rows.numel()), tuple(shape),
-           str(block_rows.device), block_rows._version, block_cols._version)
-    lay = _LAYOUTS.get(key)
-    if lay is None:
+    # Keyed on the structure tensors' identity and in-place version; each
+    # entry holds the tensors themselves, so their memory cannot be handed
+    # to other structure tensors (same address, version 0) while cached.
+    key = (_runtime.source_key(block_rows, block_cols), int(block_rows.numel()), tuple(shape),
+           str(block_rows.device))
+    hit = _LAYOUTS.get(key)
+    if hit is None:
         n_br, n_bc = (shape[0] + 31) // 32, (shape[1] + 31) // 32
         lay = build_bsr_layout(block_rows, block_cols, n_br, n_bc, block_rows.device)
         if len(_LAYOUTS) > 64:
             _LAYOUTS.clear()
-        _LAYOUTS[key] = lay
-    return lay
+        hit = _LAYOUTS[key] = (lay, block_rows, block_cols)
+    return hit[0]
 
 
 def _vt(values, block_rows, block_cols, shape, tile_size, n_blocks) -> VOIDTensor:
