@@ -95,6 +95,14 @@ def test_gpu_load_feeds_kernels(gpu):
                                   epilogue="raw_i32")
     A = oracle.Bsr(q.values.numpy(), q.scales.numpy(), case.block_rows, case.block_cols, (case.M, case.K))
     assert np.array_equal(out.cpu().numpy(), oracle.i8_acc(A, bq))
+    # The unpacked tensor's device copy follows in-place changes of its values
+    # (gathered again through the recorded order).
+    qd.values.neg_()
+    qd.values.clamp_(-127, 127)
+    out2 = void_amd.void_spmm_int8(qd, torch.from_numpy(bq).to(gpu), b_scale=torch.from_numpy(bs).to(gpu),
+                                   epilogue="raw_i32")
+    A2 = oracle.Bsr(qd.values.cpu().numpy(), q.scales.numpy(), case.block_rows, case.block_cols, (case.M, case.K))
+    assert np.array_equal(out2.cpu().numpy(), oracle.i8_acc(A2, bq))
 
 
 @pytest.mark.gpu

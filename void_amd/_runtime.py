@@ -225,6 +225,8 @@ class DeviceBsr:
         """Gather the tile values and scales again from their sources into the
         existing arrays, after the sources changed in place; the block
         structure, plans and descriptor stay valid."""
+        if self.order is None:
+            raise RuntimeError("this device copy records no gather order; build the VOID tensor again")
         dev = self.tiles.device
         v = values.to(dev)
         if v.dtype != torch.uint8:

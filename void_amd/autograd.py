@@ -46,9 +46,10 @@ def _vt(values, block_rows, block_cols, shape, tile_size, n_blocks) -> VOIDTenso
                     tile_size=tuple(tile_size), nnz_original=0, n_blocks=n_blocks, density=0.0, dtype=values.dtype)
     if n_blocks and values.is_cuda:
         ones = torch.ones(1, dtype=torch.float32, device=values.device)
-        vt._device_bsr[str(values.device)] = _runtime.make_device_bsr(
+        d = vt._device_bsr[str(values.device)] = _runtime.make_device_bsr(
             values.detach().to(torch.float32).contiguous(), ones, block_rows, block_cols, vt.shape, vt.tile_size,
             values.device, True, layout=_layout(block_rows, block_cols, vt.shape))
+        d.src_key = _runtime.source_key(values)
     return vt
 
 

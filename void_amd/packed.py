@@ -138,15 +138,20 @@ def unpack(blob: Union[bytes, bytearray, memoryview], device: Union[str, torch.d
     morton_t = torch.from_numpy(morton).to(dev).index_select(0, perm_t)
     n_br_c = (M + 31) // 32
     density = nb / (n_br_c * ((K + 31) // 32)) if M and K else 0.0
+    # BSR position p holds the tensor's tile order[p] (perm's inverse), for
+    # gathering again after in-place changes of the tensor's values.
+    order = torch.empty_like(perm_t)
+    order[perm_t] = torch.arange(nb, dtype=perm_t.dtype, device=dev)
     dbsr = _runtime.DeviceBsr(tiles=tiles_bytes.view(nb, 32, 32 * elt), scales=scales if n_sc else
                               torch.ones(1, dtype=torch.float32, device=dev), row_ptr=row_ptr, col_idx=col_idx,
                               row_ptr_host=rp_host, col_idx_host=ci_host, per_tensor=per_tensor or n_sc == 0,
-                              M=M, K=K, n_blocks=nb, n_block_rows=n_br)
+                              M=M, K=K, n_blocks=nb, n_block_rows=n_br, order=order)
     key = str(dev)
     if kind == KIND_F32:
         vals = tiles_bytes.view(torch.float32).view(nb, 32, 32).index_select(0, perm_t)
         vt = VOIDTensor(values=vals, block_rows=block_rows, block_cols=block_cols, morton_codes=morton_t,
                         shape=(M, K), tile_size=(32, 32), nnz_original=nnz, n_blocks=nb, density=density)
+        dbsr.src_key = _runtime.source_key(vals)
         vt._device_bsr[key] = dbsr
         return vt
     if kind == KIND_I8:
@@ -157,6 +162,7 @@ def unpack(blob: Union[bytes, bytearray, memoryview], device: Union[str, torch.d
         q = Int8VOIDTensor(values=vals, scales=sc, zero_points=torch.zeros(nb, dtype=torch.int8, device=dev),
                            block_rows=block_rows, block_cols=block_cols, shape=(M, K), tile_size=(32, 32),
                            n_blocks=nb, config=cfg)
+        dbsr.src_key = _runtime.source_key(vals, sc)
         q._device_bsr[key] = dbsr
         return q
     from .fp8 import FP8Config, FP8VOIDTensor, create_scaling_info
@@ -169,6 +175,7 @@ def unpack(blob: Union[bytes, bytearray, memoryview], device: Union[str, torch.d
     f8 = FP8VOIDTensor(values_fp8=vals, scaling_info=info, block_rows=block_rows, block_cols=block_cols,
                        morton_codes=morton_t, shape=(M, K), tile_size=(32, 32), nnz_original=nnz, n_blocks=nb,
                        density=density)
+    dbsr.src_key = _runtime.source_key(vals, info.scale)
     f8._device_bsr[key] = dbsr
     return f8
 
