@@ -44,7 +44,7 @@ def _abs_bound(A, bq, bs):
     return oracle.i8_per_block(Aabs, np.abs(bq.astype(np.int16)).clip(0, 127).astype(np.int8), np.abs(bs))
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(64))
 def test_random_int8(gpu, kernel, seed):
     case, rng = _case(seed)
     vt = cases.make_void_tensor(case, "cpu")
@@ -74,7 +74,7 @@ def test_random_int8(gpu, kernel, seed):
         assert np.array_equal(rm.cpu().numpy().view(np.int32), want.view(np.int32)), (case.M, case.K, case.N)
 
 
-@pytest.mark.parametrize("seed", range(24, 32))
+@pytest.mark.parametrize("seed", list(range(24, 32)) + list(range(64, 72)))
 def test_random_fp8(gpu, kernel, seed):
     case, rng = _case(seed)
     vt = cases.make_void_tensor(case, "cpu")
