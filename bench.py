@@ -62,6 +62,9 @@ def parse():
                          "(gradient on the config's nonzero tiles); floor: a tiny kernel and plain copies "
                          "of c2's byte count in the same cold harness")
     ap.add_argument("--epilogue", default=None, help="int8 epilogue (default per_block)")
+    ap.add_argument("--dtype", default="f32", choices=["f32", "bf16", "f16"],
+                    help="--op float: tile and B dtype (bf16 / f16 run the 16-bit MFMA kernel, output in the "
+                         "same dtype)")
     ap.add_argument("--chunk", type=int, default=None, help="override the Stream-K chunk")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--profile", action="store_true", help="no CPU leg, no flush: for rocprofv3 runs")
@@ -270,8 +273,10 @@ FP32_PEAK_TFLOPS = 157.3  # dense MFMA fp32, MI355X
 
 
 def bench_float(args, dev):
-    """void_spmm on fp32 tiles and fp32 B of a config (the reference's float
-    path), fp32 MFMA; CPU baseline: the torch-CPU tile path in fp32."""
+    """void_spmm on the float tiles and B of a config (the reference's float
+    path): fp32 (fp32 MFMA) or, with --dtype bf16 / f16, both operands and the
+    output in that dtype (16-bit MFMA); CPU baseline: the torch-CPU tile path
+    in fp32."""
     import torch
 
     import cases
@@ -280,6 +285,10 @@ def bench_float(args, dev):
     case = {"c2": cases.c2_int8, "c3": cases.c3_fp8, "c4": cases.c4_powerlaw, "c5": cases.c5_ffn}[args.config]()
     vt = cases.make_void_tensor(case, "cpu").to(dev)
     B = torch.from_numpy(case.b).to(dev)
+    dt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[args.dtype]
+    esz = 4 if dt == torch.float32 else 2
+    if args.op == "float" and dt != torch.float32:
+        vt, B = vt.to_dtype(dt), B.to(dt)
     nb = vt.n_blocks
     ops = 2.0 * nb * 1024 * case.N
     if args.op == "sddmm":
@@ -293,15 +302,16 @@ def bench_float(args, dev):
         run = lambda: _runtime.sddmm_tiles(G, B, rows, cols, (case.M, case.K), torch.float32, layout=lay)
         nbytes = nb * (4096 + 8) + 4 * case.M * case.N + 4 * case.K * case.N
     else:
-        out = torch.empty(case.M, case.N, device=dev)
+        out = torch.empty(case.M, case.N, device=dev, dtype=dt)
         run = lambda: void_amd.void_spmm(vt, B, out=out)
-        nbytes = nb * (4096 + 4) + 4 * (vt.block_grid[0] + 1) + 4 * case.K * case.N + 4 * case.M * case.N
+        nbytes = nb * (1024 * esz + 4) + 4 * (vt.block_grid[0] + 1) + esz * case.K * case.N + esz * case.M * case.N
     cold, hot, wall = time_gpu({"run": run}, args.steps, args.warmup, flush=True)
-    t_mem, t_ops = nbytes / (HBM_PEAK_GBS * 1e9), ops / (FP32_PEAK_TFLOPS * 1e12)
+    peak = FP32_PEAK_TFLOPS if esz == 4 or args.op == "sddmm" else BF16_PEAK_TFLOPS
+    t_mem, t_ops = nbytes / (HBM_PEAK_GBS * 1e9), ops / (peak * 1e12)
     tflops = ops / (cold * 1e-3) / 1e12
     if t_ops >= t_mem:
-        roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(tflops / FP32_PEAK_TFLOPS, 4)}
+        roof = {"bound": "mfma", "achieved": round(tflops, 2), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(tflops / peak, 4)}
     else:
         gbs = nbytes / (cold * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -348,10 +358,11 @@ def bench_float(args, dev):
                "kind": "port", "ms": round(med * 1e3, 3),
                "sample": f"full {args.config} problem in fp32, torch CPU tile bmm + index_add, median of {len(times) - 1} reps"}
     what = "SDDMM backward of A (void_sddmm_rows_f32)" if args.op == "sddmm" else "BSpMM (void_spmm)"
-    line = {"metric": f"FP32 {what} effective TFLOP/s, {case.name} in fp32", "value": round(tflops, 3),
+    dname = "f32" if args.op == "sddmm" else args.dtype
+    line = {"metric": f"{dname.upper()} {what} effective TFLOP/s, {case.name} in {dname}", "value": round(tflops, 3),
             "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(cold, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "f32", "data": "synthetic (seeded generators of BASELINE.json configs)",
+            "dtype": dname, "data": "synthetic (seeded generators of BASELINE.json configs)",
             "config": {"workload": case.name, "op": args.op, "M": case.M, "K": case.K, "N": case.N, "n_tiles": nb,
                        "cache": "cold (1 GiB overwrite between steps)"},
             "roofline": roof, "cpu_baseline": cpu,

@@ -267,6 +267,21 @@ int void_spmm_fp8_f32b(const void_bsr_desc* a, const void_dense_args* d, const v
 int void_spmm_f32(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
                   void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Float SpMM on 16-bit tensors: bf16 tiles times bf16 B (void_spmm_bf16) or
+ * fp16 tiles times fp16 B (void_spmm_f16) on the 16-bit MFMA (exact
+ * products, fp32 accumulation), then bias, activation and conversion to
+ * d->out_dtype (f32, bf16 or f16).  Replaces void_spmm_kernel + void_spmm
+ * (void/ops.py:148-213, whose tl.dot takes 16-bit operands as they are) and
+ * void_spmm_activation_kernel (void/fusion.py:98-198) for VOID tensors
+ * whose values and B share a 16-bit dtype.  a->tiles holds 16-bit tiles
+ * (2048 bytes each); scales unused.  B and C row-major with 16-byte aligned
+ * rows, N % 8 == 0 (else VOID_ERR_UNSUPPORTED); plan items of at most 64
+ * tiles; workspace as for void_spmm_int8. */
+int void_spmm_bf16(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
+                   void* workspace, size_t workspace_bytes, hipStream_t stream);
+int void_spmm_f16(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
+                  void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* ---- Quantisers on the path's input side (one wave per tile) ---------- */
 
 /* Per-tile symmetric INT8 of n_tiles fp32 32x32 tiles (tile t at

@@ -45,11 +45,9 @@ def _vt(values, block_rows, block_cols, shape, tile_size, n_blocks) -> VOIDTenso
                     morton_codes=torch.empty(0, dtype=torch.int64, device=values.device), shape=tuple(shape),
                     tile_size=tuple(tile_size), nnz_original=0, n_blocks=n_blocks, density=0.0, dtype=values.dtype)
     if n_blocks and values.is_cuda:
-        ones = torch.ones(1, dtype=torch.float32, device=values.device)
-        d = vt._device_bsr[str(values.device)] = _runtime.make_device_bsr(
-            values.detach().to(torch.float32).contiguous(), ones, block_rows, block_cols, vt.shape, vt.tile_size,
-            values.device, True, layout=_layout(block_rows, block_cols, vt.shape))
-        d.src_key = _runtime.source_key(values)
+        # The device copy (fp32 or 16-bit, as the SpMM needs) is built on
+        # first use from this cached block-row order.
+        vt._bsr_layout = _layout(block_rows, block_cols, vt.shape)
     return vt
 
 

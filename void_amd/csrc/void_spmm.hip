@@ -66,8 +66,9 @@ typedef float v2f __attribute__((ext_vector_type(2)));
 
 // Tile element types: int8 and E4M3 tiles times a B of the same type; fp32
 // tiles times fp32 B (float SpMM); E4M3 tiles times fp32 B (kEltFp8F32, the
-// reference's FP8 SpMM with a float B).
-enum Elt { kEltI8 = 0, kEltFp8 = 1, kEltF32 = 2, kEltFp8F32 = 3 };
+// reference's FP8 SpMM with a float B); bf16 or fp16 tiles times a B of the
+// same type (float SpMM on 16-bit tensors, on the 16-bit MFMA).
+enum Elt { kEltI8 = 0, kEltFp8 = 1, kEltF32 = 2, kEltFp8F32 = 3, kEltBf16 = 4, kEltF16 = 5 };
 
 struct Params {
   const uint8_t* tiles;
@@ -1025,7 +1026,15 @@ struct Accum1<kEltF32, EPI> {
 template <int EPI>
 struct Accum1<kEltFp8F32, EPI> : Accum1<kEltF32, EPI> {};
 
+// bf16 / fp16 tiles: fp32 accumulation, no per-tile scales, product in the
+// ring loop.
+template <int EPI>
+struct Accum1<kEltBf16, EPI> : Accum1<kEltF32, EPI> {};
+template <int EPI>
+struct Accum1<kEltF16, EPI> : Accum1<kEltF32, EPI> {};
+
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8hf __attribute__((ext_vector_type(8)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
 // Two floats rounded to bf16 (nearest even, v_cvt_pk_bf16_f32), packed.
@@ -1113,13 +1122,16 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
   constexpr bool kInt = A::kInt;
   constexpr bool kF32 = ELT == kEltF32;                     // fp32 A tiles
   constexpr bool kBF32 = kF32 || ELT == kEltFp8F32;         // fp32 B slabs
-  static_assert(!kBF32 || DMA, "fp32 B only on the LDS-DMA ring");
-  constexpr bool kScales = (EPI == VOID_EPI_PER_BLOCK) && !kF32;
+  constexpr bool k16 = ELT == kEltBf16 || ELT == kEltF16;   // 16-bit tiles and B
+  constexpr bool kFloat = kF32 || k16;                      // unscaled float tiles
+  static_assert(!(kBF32 || k16) || DMA, "fp32 and 16-bit B only on the LDS-DMA ring");
+  constexpr bool kScales = (EPI == VOID_EPI_PER_BLOCK) && !kFloat;
   // fp32 B: 4 bytes per element, one tile per stage (a 16 KB B slab, and 4 KB
-  // of A for fp32 tiles or 1 KB for E4M3 ones), so the ring keeps its 40 KB.
-  constexpr int kEsz = kF32 ? 4 : 1;    // A
-  constexpr int kBEsz = kBF32 ? 4 : 1;  // B
-  constexpr int kStageTiles = kBF32 ? 1 : RT;
+  // of A for fp32 tiles or 1 KB for E4M3 ones); 16-bit: two tiles per stage
+  // (8 KB slab + 2 KB tile each).  Either way the ring keeps its 40 KB.
+  constexpr int kEsz = kF32 ? 4 : k16 ? 2 : 1;    // A
+  constexpr int kBEsz = kBF32 ? 4 : k16 ? 2 : 1;  // B
+  constexpr int kStageTiles = kBF32 ? 1 : k16 ? 2 : RT;
 
   // Tile slots: two batches of the register-staged loop, or the LDS-DMA ring.
   // KS = 2: two groups of 4 waves, each with its own ring, take alternate
@@ -1318,6 +1330,26 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
       const int r = 8 * wave + 2 * k + (lane >> 5);
       return (kb_last < 0 || r < p.K - kb_last * kTile) ? voffs_f[k] : kOutOfRange;
     };
+    // 16-bit B: a slab row is 256 bytes (16 chunks); wave w fills rows 8 w ..
+    // 8 w + 7, four rows per load.  LDS chunk q of row r holds global chunk
+    // q ^ ((r & 3) << 2), so the four rows of one transposed read sit in four
+    // different bank quarters.  16-bit A: a tile is 32 rows of 64 bytes; wave
+    // w loads half w & 1 (16 rows) of the stage's tile w >> 1, and LDS chunk
+    // q of row r holds global chunk q ^ ((r >> 2) & 3).
+    int voffs_h[2] = {0, 0}, voffs_h_last[2] = {0, 0};
+    int voff_ah = 0;
+    if constexpr (k16) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int r = 8 * wave + 4 * k + (lane >> 4);
+        int cb = panel * kPanel * 2 + 16 * ((lane & 15) ^ ((r & 3) << 2));
+        cb = cb < p.N * 2 ? cb : 0;  // past N: any valid 16 bytes, never stored
+        voffs_h[k] = (int)(r * p.ldb * 2) + cb;
+        voffs_h_last[k] = (kb_last < 0 || r < p.K - kb_last * kTile) ? voffs_h[k] : kOutOfRange;
+      }
+      const int ar = 16 * (wave & 1) + (lane >> 2);
+      voff_ah = ar * (kTile * 2) + 16 * ((lane & 3) ^ ((ar >> 2) & 3));
+    }
     // Stages of the item; wave group sg takes global stages sg, sg + KS, ...
     // (ns of them), and both groups run ns_loop iterations so that they meet
     // at every barrier.
@@ -1326,7 +1358,7 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     const int ns_loop = (ns_all + KS - 1) / KS;
     // The first RT waves also load one A tile per stage (wave 0 the one E4M3
     // tile of a stage with fp32 B; every wave a quarter of an fp32 tile).
-    const bool a_wave = wave < (kBF32 ? 1 : RT);
+    const bool a_wave = wave < (kBF32 ? 1 : k16 ? kWaves : RT);
     // Stages issued before the windows land (the prologue, s < kDmaStages - 1,
     // a constant after unrolling) read their columns from the work item
     // (tiles below 16); later ones from colw.
@@ -1351,6 +1383,26 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     auto issue_stage = [&](int s) {
       const int slot0 = (s % kDmaStages) * kStageTiles;
       const int base = (s * KS + sg) * kStageTiles;
+      if constexpr (k16) {
+        // One A load (half a tile) and four B loads per wave: 5 per stage.
+        {
+          const int idx = base + (wave >> 1);
+          const bool live = idx < nt;
+          dma_b128(da, &a_ring[slot0 + (wave >> 1)][(wave & 1) * 64], live ? voff_ah : kOutOfRange,
+                   (begin + (live ? idx : 0)) * (kTile * kTile * 2));
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int kb = stage_col(s, u);
+          const bool live = base + u < nt;
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const int vo = live ? (kb == kb_last ? voffs_h_last[k] : voffs_h[k]) : kOutOfRange;
+            dma_b128(db, &b_ring[slot0 + u][(8 * wave + 4 * k) * (kPanel * 2)], vo, kb * b_kstride);
+          }
+        }
+        return;
+      }
       if constexpr (kBF32) {
         const bool live = base < nt;
         if constexpr (kF32) {
@@ -1395,7 +1447,7 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     for (int s = 0; s < ns_loop; ++s) {
       // Past this group's last stage (s >= ns) ahead is negative: wait for all.
       const int ahead = min(ns - 1, s + kDmaStages - 2) - s;  // stages issued after s
-      if (kF32) wait_stages<5>(ahead);
+      if (kF32 || k16) wait_stages<5>(ahead);
       else if (kBF32) {
         if (a_wave) wait_stages<5>(ahead);
         else wait_stages<4>(ahead);
@@ -1433,6 +1485,46 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
         for (int s2 = 0; s2 < 16; ++s2)
           acc = __builtin_amdgcn_mfma_f32_32x32x2f32(af[s2 >> 2][s2 & 3], bf[s2], acc, 0, 0, 0);
+      } else if constexpr (k16) {
+        // 16-bit tiles on v_mfma_f32_32x32x16_{bf16,f16}, two per tile: MFMA h
+        // takes k = 16 h + 8 g .. + 7 for lane (i, g), A row i (one 16-byte
+        // read) and B column 32 wave + i (two ds_read_b64_tr_b16, each giving
+        // four k of one column: the 16 lanes of a read fetch a 4-row x
+        // 16-column block, 8 bytes each in row-major order, and lane t gets
+        // column t).  Tiles past the item's end were loaded as zeros.
+        const int i = j & 15;
+        typedef short v4h16 __attribute__((ext_vector_type(4)));
+        typedef short v8h16 __attribute__((ext_vector_type(8)));
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const uint8_t* as = reinterpret_cast<const uint8_t*>(&a_ring[slot0 + u][0]);
+          const uint8_t* bs = &b_ring[slot0 + u][0];
+          v4i av[2];
+          v8h16 bv[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            av[h] = *reinterpret_cast<const v4i*>(as + j * (kTile * 2) + (((2 * h + g) ^ ((j >> 2) & 3)) << 4));
+            v4h16 t[2];
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+              const int row = 16 * h + 8 * g + 4 * r + (i >> 2);
+              const int gq = 4 * wave + 2 * (j >> 4) + ((i & 3) >> 1);
+              const uint8_t* a = bs + row * (kPanel * 2) + ((gq ^ ((row & 3) << 2)) << 4) + 8 * (i & 1);
+              t[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (__attribute__((address_space(3))) v4h16*)(const_cast<uint8_t*>(a)));
+            }
+            bv[h] = v8h16{t[0][0], t[0][1], t[0][2], t[0][3], t[1][0], t[1][1], t[1][2], t[1][3]};
+          }
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            if constexpr (ELT == kEltBf16)
+              acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, av[h]),
+                                                            __builtin_bit_cast(v8bf, bv[h]), acc, 0, 0, 0);
+            else
+              acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8hf, av[h]),
+                                                           __builtin_bit_cast(v8hf, bv[h]), acc, 0, 0, 0);
+          }
+        }
       } else if constexpr (ELT == kEltFp8F32) {
         // E4M3 tile times fp32 B on the bf16 MFMA: lane (i, g) holds A row i,
         // k = 16 g .. 16 g + 15 (its 16 codes, decoded exactly to bf16) and B
@@ -1663,7 +1755,7 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     }
     mul = (re > rb) ? __fdiv_rn(S, (float)(re - rb)) : 0.f;
   } else if constexpr (EPI == VOID_EPI_PER_BLOCK) {
-    mul = kF32 ? 1.f : sb;
+    mul = kFloat ? 1.f : sb;
   }
 
   constexpr int esz = (OUT == VOID_DT_F32 || OUT == VOID_DT_I32) ? 4 : 2;
@@ -2277,7 +2369,8 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
   if (!d->c) return fail(VOID_ERR_ARG, "null output pointer");
   if (!items || n_items <= 0) return fail(VOID_ERR_ARG, "empty work list for M=%d", a->M);
   if (!a->row_ptr) return fail(VOID_ERR_ARG, "null row_ptr");
-  if (a->n_blocks > 0 && (!a->tiles || !a->col_idx || (!a->scales && elt != kEltF32) || !d->b))
+  const bool unscaled = elt == kEltF32 || elt == kEltBf16 || elt == kEltF16;
+  if (a->n_blocks > 0 && (!a->tiles || !a->col_idx || (!a->scales && !unscaled) || !d->b))
     return fail(VOID_ERR_ARG, "null tile, column, scale or B pointer");
   if (d->ldc < d->N) return fail(VOID_ERR_ARG, "ldc %lld < N %d", (long long)d->ldc, d->N);
   if (d->b_col_major ? d->ldb < a->K : d->ldb < d->N)
@@ -2290,7 +2383,7 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
     return fail(VOID_ERR_UNSUPPORTED, "fp8 SpMM supports only the per-block epilogue");
   const bool b_f32 = elt == kEltF32 || elt == kEltFp8F32;
   if (b_f32 && d->b_col_major) return fail(VOID_ERR_UNSUPPORTED, "an fp32 B must be row-major");
-  if (d->bias_per_row && elt != kEltF32)
+  if (d->bias_per_row && !unscaled)
     return fail(VOID_ERR_UNSUPPORTED, "a per-row bias is supported by the float SpMM only");
   if (b_f32 && plan->chunk_tiles > 64)
     return fail(VOID_ERR_ARG, "an fp32 B takes work items of at most 64 tiles (chunk_tiles %d)", plan->chunk_tiles);
@@ -2391,6 +2484,37 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
       case VOID_DT_F16: return launch_cg<kEltFp8F32, VOID_EPI_PER_BLOCK, VOID_DT_F16, false, true>(p, grid, stream);
       default: return fail(VOID_ERR_UNSUPPORTED, "E4M3 x fp32 SpMM writes f32, bf16 or f16");
     }
+  }
+  if (elt == kEltBf16 || elt == kEltF16) {
+    // 16-bit tiles and B: the LDS-DMA ring only (row-major B and C with
+    // 16-byte aligned rows, N % 8 == 0, items of at most 64 tiles, 31-bit
+    // byte offsets).  The Python wrapper takes the fp32 kernel otherwise.
+    const int64_t lim = (int64_t)1 << 31;
+    const int esz = (d->out_dtype == VOID_DT_BF16 || d->out_dtype == VOID_DT_F16) ? 2 : 4;
+    if (d->b_col_major || !(c_ok && (bu % 16 == 0) && (d->ldb % 8 == 0) && (d->N % 8 == 0)))
+      return fail(VOID_ERR_UNSUPPORTED, "16-bit SpMM needs a row-major B, 16-byte aligned B and C rows and N %% 8 == 0");
+    if (plan->chunk_tiles > kCgMaxTiles)
+      return fail(VOID_ERR_ARG, "16-bit SpMM takes work items of at most %d tiles (chunk_tiles %d)", kCgMaxTiles,
+                  plan->chunk_tiles);
+    if (!((int64_t)a->n_blocks * kTile * kTile * 2 < lim && (int64_t)((a->K + kTile - 1) / kTile) * kTile * d->ldb * 2 < lim &&
+          (int64_t)a->M * d->ldc * esz < lim))
+      return fail(VOID_ERR_UNSUPPORTED, "16-bit SpMM operands must stay below 2 GiB");
+    if (elt == kEltBf16) {
+      switch (d->out_dtype) {
+        case VOID_DT_F32: return launch_cg<kEltBf16, VOID_EPI_PER_BLOCK, VOID_DT_F32, false, true>(p, grid, stream);
+        case VOID_DT_BF16: return launch_cg<kEltBf16, VOID_EPI_PER_BLOCK, VOID_DT_BF16, false, true>(p, grid, stream);
+        case VOID_DT_F16: return launch_cg<kEltBf16, VOID_EPI_PER_BLOCK, VOID_DT_F16, false, true>(p, grid, stream);
+        default: break;
+      }
+    } else {
+      switch (d->out_dtype) {
+        case VOID_DT_F32: return launch_cg<kEltF16, VOID_EPI_PER_BLOCK, VOID_DT_F32, false, true>(p, grid, stream);
+        case VOID_DT_BF16: return launch_cg<kEltF16, VOID_EPI_PER_BLOCK, VOID_DT_BF16, false, true>(p, grid, stream);
+        case VOID_DT_F16: return launch_cg<kEltF16, VOID_EPI_PER_BLOCK, VOID_DT_F16, false, true>(p, grid, stream);
+        default: break;
+      }
+    }
+    return fail(VOID_ERR_UNSUPPORTED, "16-bit SpMM writes f32, bf16 or f16");
   }
   if (elt == kEltF32) {
     const bool vec = c_ok && (bu % 16 == 0) && (d->ldb % 4 == 0) && (d->N % 4 == 0);
@@ -2800,6 +2924,18 @@ int void_spmm_f32(const void_bsr_desc* a, const void_dense_args* d, const void_p
                   void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (d && d->out_dtype == VOID_DT_I32) return fail(VOID_ERR_UNSUPPORTED, "float SpMM writes f32, bf16 or f16");
   return run(kEltF32, a, d, VOID_EPI_PER_BLOCK, plan, workspace, workspace_bytes, stream);
+}
+
+int void_spmm_bf16(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
+                   void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (d && d->out_dtype == VOID_DT_I32) return fail(VOID_ERR_UNSUPPORTED, "16-bit SpMM writes f32, bf16 or f16");
+  return run(kEltBf16, a, d, VOID_EPI_PER_BLOCK, plan, workspace, workspace_bytes, stream);
+}
+
+int void_spmm_f16(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
+                  void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (d && d->out_dtype == VOID_DT_I32) return fail(VOID_ERR_UNSUPPORTED, "16-bit SpMM writes f32, bf16 or f16");
+  return run(kEltF16, a, d, VOID_EPI_PER_BLOCK, plan, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

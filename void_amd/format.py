@@ -123,23 +123,27 @@ class VOIDTensor:
     density: float
     dtype: torch.dtype = torch.float32
     _device_bsr: dict = field(default_factory=dict, repr=False, compare=False)
+    # Block-row order of the tiles (a BsrLayout), when a caller already has it.
+    _bsr_layout: object = field(default=None, repr=False, compare=False)
 
-    def device_bsr(self):
-        """Block-row-major fp32 device copy of the tiles for the float kernel
-        (built once per device, gathered again when the values change in
-        place, since the reference reads them on every call)."""
+    def device_bsr(self, dtype: torch.dtype = torch.float32):
+        """Block-row-major device copy of the tiles in ``dtype`` (fp32 for the
+        fp32 kernel, bf16 / fp16 for the 16-bit one), built once per device
+        and dtype and gathered again when the values change in place, since
+        the reference reads them on every call."""
         from . import _runtime
-        key = str(self.values.device)
+        key = str(self.values.device) if dtype == torch.float32 else f"{self.values.device}/{dtype}"
         src = _runtime.source_key(self.values)
         d = self._device_bsr.get(key)
         if d is None:
             ones = torch.ones(1, dtype=torch.float32, device=self.values.device)
-            d = _runtime.make_device_bsr(self.values.to(torch.float32).contiguous(), ones, self.block_rows,
-                                         self.block_cols, self.shape, self.tile_size, self.values.device, True)
+            d = _runtime.make_device_bsr(self.values.detach().to(dtype).contiguous(), ones, self.block_rows,
+                                         self.block_cols, self.shape, self.tile_size, self.values.device, True,
+                                         layout=self._bsr_layout)
             d.src_key = src
             self._device_bsr[key] = d
         elif d.src_key != src:
-            d.refresh(self.values.to(torch.float32).contiguous(), d.scales)
+            d.refresh(self.values.detach().to(dtype).contiguous(), d.scales)
             d.src_key = src
         return d
 

@@ -1,5 +1,6 @@
-"""Float SpMM on VOID tiles (void/ops.py:148-213): C = A @ B with fp32
-tiles, on the fp32 MFMA kernel of libvoid_amd.so (void_spmm_f32)."""
+"""Float SpMM on VOID tiles (void/ops.py:148-213): C = A @ B on the MFMA
+kernels of libvoid_amd.so: void_spmm_bf16 / void_spmm_f16 when the tiles and
+B share a 16-bit dtype, void_spmm_f32 (fp32 tiles and B) otherwise."""
 
 from __future__ import annotations
 
@@ -13,6 +14,21 @@ from . import _lib, _runtime
 # Longest work item of the float kernel: it holds an item's block columns in
 # one register per lane.
 F32_CHUNK = 64
+
+
+_K16 = {torch.bfloat16: "void_spmm_bf16", torch.float16: "void_spmm_f16"}
+
+
+def _fits16(a, b: torch.Tensor, c: torch.Tensor) -> bool:
+    """What void_spmm_bf16 / void_spmm_f16 take: row-major B and C with
+    16-byte aligned rows, N % 8 == 0, and operands within 31-bit offsets."""
+    M, K = a.shape
+    N = b.shape[1]
+    lim = 1 << 31
+    return (N % 8 == 0 and b.stride(0) % 8 == 0 and b.data_ptr() % 16 == 0 and
+            c.data_ptr() % 16 == 0 and c.stride(0) % 4 == 0 and
+            a.n_blocks * 2048 < lim and ((K + 31) // 32) * 32 * b.stride(0) * 2 < lim and
+            M * c.stride(0) * c.element_size() < lim)
 
 
 def float_spmm(a, b: torch.Tensor, *, out: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
@@ -42,14 +58,27 @@ def float_spmm(a, b: torch.Tensor, *, out: Optional[torch.Tensor] = None, bias: 
     _runtime.require_gpu(a.values, "A")
     if a.values.device != b.device:
         raise ValueError(f"A on {a.values.device}, B on {b.device}")
-    b32 = b.to(torch.float32).contiguous()
     if bias is not None:
         if bias.shape != ((M,) if bias_per_row else (N,)):
             raise ValueError(f"bias must be [{M if bias_per_row else N}]")
         bias = bias.to(device=b.device, dtype=torch.float32).contiguous()
-    dbsr = a.device_bsr()
     lib = _lib.lib()
     target = out if (out.stride(1) == 1 and out.stride(0) >= N) else torch.empty_like(out)
+    # 16-bit tiles times a B of the same dtype run on the 16-bit MFMA (the
+    # reference's tl.dot takes them as they are); everything else on the fp32
+    # kernel, whose products of widened 16-bit values are the same numbers.
+    entry = "void_spmm_f32"
+    bk = None
+    if a.values.dtype == b.dtype and b.dtype in _K16:
+        bk = b if b.stride(1) == 1 else b.contiguous()
+        if not _fits16(a, bk, target):
+            bk = None
+    if bk is not None:
+        entry = _K16[b.dtype]
+        dbsr = a.device_bsr(b.dtype)
+    else:
+        bk = b.to(torch.float32).contiguous()
+        dbsr = a.device_bsr()
     if plan is None:
         plan = dbsr.plan(F32_CHUNK)
     elif plan.chunk > F32_CHUNK:
@@ -57,15 +86,15 @@ def float_spmm(a, b: torch.Tensor, *, out: Optional[torch.Tensor] = None, bias: 
     ws, ws_bytes = plan.workspace(N, out.device)
     cplan = _lib.Plan(items=plan.items.data_ptr(), n_items=plan.n_items, n_split_tiles=plan.n_split_tiles,
                       n_slots=plan.n_slots, chunk_tiles=plan.chunk)
-    dense = _lib.DenseArgs(b=b32.data_ptr(), ldb=b32.stride(0), b_col_major=0, N=N, b_scale=1.0, b_scale_vec=None,
+    dense = _lib.DenseArgs(b=bk.data_ptr(), ldb=bk.stride(0), b_col_major=0, N=N, b_scale=1.0, b_scale_vec=None,
                            bias=bias.data_ptr() if bias is not None else None, c=target.data_ptr(),
                            ldc=target.stride(0), out_dtype=_runtime.out_code(target.dtype), activation=activation,
                            bias_per_row=int(bias_per_row))
     desc = dbsr.desc()
-    st = lib.void_spmm_f32(ctypes.byref(desc), ctypes.byref(dense), ctypes.byref(cplan),
-                           ws.data_ptr() if ws is not None else None, ws_bytes,
-                           torch.cuda.current_stream(out.device).cuda_stream)
-    _lib.check(st, "void_spmm_f32")
+    st = getattr(lib, entry)(ctypes.byref(desc), ctypes.byref(dense), ctypes.byref(cplan),
+                             ws.data_ptr() if ws is not None else None, ws_bytes,
+                             torch.cuda.current_stream(out.device).cuda_stream)
+    _lib.check(st, entry)
     if target is not out:
         out.copy_(target)
     return out
