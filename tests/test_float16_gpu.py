@@ -177,3 +177,25 @@ def test_fused_linear_bf16(gpu):
     ref = A @ B + bias.double().cpu().numpy()[:, None]
     absprod = np.abs(A) @ np.abs(B) + np.abs(bias.double().cpu().numpy())[:, None]
     _check(out, ref, absprod, _n_row(vt) + 1, torch.bfloat16)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_spmm16_random(gpu, seed):
+    """Seeded random ragged shapes and densities (one tile to dense rows,
+    N a multiple of 8 so that the 16-bit kernel runs), bf16 and fp16 by
+    seed parity, default and forced-small chunks (split rows)."""
+    rng = np.random.default_rng(5000 + seed)
+    M, K = int(rng.integers(1, 700)), int(rng.integers(1, 2200))
+    N = int(rng.choice([8, 16, 40, 64, 128, 136, 256, 384, 520]))
+    nbr, nbc = -(-M // 32), -(-K // 32)
+    case = cases.uniform_blocks(M, K, N, int(rng.integers(1, nbr * nbc + 1)), seed=seed)
+    dtype = torch.bfloat16 if seed % 2 == 0 else torch.float16
+    print(f"spmm16 random seed={seed} M={M} K={K} N={N} tiles={len(case.block_rows)} {dtype}", flush=True)
+    vt = _vt16(case, dtype, gpu)
+    Bt = torch.from_numpy(case.b).to(dtype)
+    from void_amd.ops import float_spmm
+    plan = vt.device_bsr(dtype).plan(int(rng.choice([8, 24, 64]))) if seed % 3 == 0 else None
+    out = float_spmm(vt, Bt.to(gpu), plan=plan)
+    assert _used_16bit(vt, dtype)
+    A, B = _dense(vt), Bt.double().numpy()
+    _check(out, A @ B, np.abs(A) @ np.abs(B), _n_row(vt), dtype)

@@ -115,3 +115,14 @@ def test_graph_float(gpu):
     vt = cases.make_void_tensor(case, "cpu").to(gpu)
     b = torch.from_numpy(case.b).to(gpu)
     _capture_and_check(lambda: void_amd.void_spmm(vt, b), _other(gpu))
+
+
+def test_graph_bf16(gpu):
+    """16-bit float tiles and B (void_spmm_bf16), split rows included."""
+    case = cases.uniform_blocks(512, 4096, 256, 900, seed=15)
+    vt = cases.make_void_tensor(case, "cpu").to_dtype(torch.bfloat16).to(gpu)
+    b = torch.from_numpy(case.b).to(torch.bfloat16).to(gpu)
+    from void_amd.ops import float_spmm
+    plan = vt.device_bsr(torch.bfloat16).plan(12)
+    assert plan.n_split_tiles > 0
+    _capture_and_check(lambda: float_spmm(vt, b, plan=plan), _other(gpu))
