@@ -25,6 +25,17 @@ ROUND = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11, torch.float32: 0.
 ABS = {torch.bfloat16: 0.0, torch.float16: 2.0 ** -25, torch.float32: 0.0}
 
 
+@pytest.fixture(params=["default", "cgd", "cgdk"])
+def k16(request, monkeypatch):
+    """Ring shapes of the 16-bit kernel: the default choice, one ring per
+    workgroup, two rings per 8-wave workgroup."""
+    if request.param == "default":
+        monkeypatch.delenv("VOID_AMD_KERNEL", raising=False)
+    else:
+        monkeypatch.setenv("VOID_AMD_KERNEL", request.param)
+    return request.param
+
+
 def _vt16(case, dtype, dev):
     vt = cases.make_void_tensor(case, "cpu")
     vt = dataclasses.replace(vt, values=vt.values.to(dtype), dtype=dtype, _device_bsr={})
@@ -55,7 +66,7 @@ def _used_16bit(vt, dtype):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M,K,N,n_tiles,seed", [(4096, 4096, 512, 1638, 0), (1024, 2048, 256, 900, 3),
                                                 (96, 96, 64, 9, 1), (4096, 4096, 2048, 3277, 4)])
-def test_spmm16(gpu, dtype, M, K, N, n_tiles, seed):
+def test_spmm16(gpu, k16, dtype, M, K, N, n_tiles, seed):
     case = cases.uniform_blocks(M, K, N, n_tiles, seed=seed)
     print(f"spmm16 {dtype} M={M} K={K} N={N} tiles={n_tiles}", flush=True)
     vt = _vt16(case, dtype, gpu)
@@ -81,7 +92,7 @@ def test_spmm16_f32_output(gpu, dtype):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M,K,N", [(333, 555, 64), (100, 70, 40), (64, 96, 136), (1000, 70, 264),
                                    (130, 250, 36), (70, 40, 257)])
-def test_spmm16_ragged(gpu, dtype, M, K, N):
+def test_spmm16_ragged(gpu, k16, dtype, M, K, N):
     # K not a multiple of 32 (the last slab loads no rows past K); N % 8 != 0
     # takes the fp32 kernel, with the same bound.
     rng = np.random.default_rng(M + K + N)
@@ -111,7 +122,7 @@ def test_spmm16_strided_b_and_out(gpu):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_spmm16_split_rows(gpu, dtype):
+def test_spmm16_split_rows(gpu, k16, dtype):
     # Rows of 100 tiles: the 64-tile items split, exercising the fix-up.
     rng = np.random.default_rng(7)
     rows, cols = [], []
@@ -180,7 +191,7 @@ def test_fused_linear_bf16(gpu):
 
 
 @pytest.mark.parametrize("seed", range(24))
-def test_spmm16_random(gpu, seed):
+def test_spmm16_random(gpu, k16, seed):
     """Seeded random ragged shapes and densities (one tile to dense rows,
     N a multiple of 8 so that the 16-bit kernel runs), bf16 and fp16 by
     seed parity, default and forced-small chunks (split rows)."""

@@ -1116,8 +1116,8 @@ template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false, int RT = kDmaT
 __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     DMA ? (KS > 1 ? 4 : dma_waves_per_eu(RT)) : 2, DMA ? (KS > 1 ? 4 : dma_waves_per_eu(RT)) : 2))) void spmm_cg_kernel(Params p) {
   static_assert(!(DMA && BCOL), "the LDS-DMA ring is for row-major B");
-  static_assert(KS == 1 || (DMA && (ELT == kEltI8 || ELT == kEltFp8) && KS == 2),
-                "the two-ring split is for int8 / fp8 on the LDS-DMA ring");
+  static_assert(KS == 1 || (DMA && (ELT == kEltI8 || ELT == kEltFp8 || ELT == kEltBf16 || ELT == kEltF16) && KS == 2),
+                "the two-ring split is for int8 / fp8 / 16-bit tiles on the LDS-DMA ring");
   using A = Accum1<ELT, EPI>;
   constexpr bool kInt = A::kInt;
   constexpr bool kF32 = ELT == kEltF32;                     // fp32 A tiles
@@ -2499,22 +2499,29 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
     if (!((int64_t)a->n_blocks * kTile * kTile * 2 < lim && (int64_t)((a->K + kTile - 1) / kTile) * kTile * d->ldb * 2 < lim &&
           (int64_t)a->M * d->ldc * esz < lim))
       return fail(VOID_ERR_UNSUPPORTED, "16-bit SpMM operands must stay below 2 GiB");
-    if (elt == kEltBf16) {
+    // Ring shape as for int8: two rings per 8-wave workgroup for one-round
+    // grids and split plans below four rounds, one ring otherwise
+    // (VOID_AMD_KERNEL=cgdk / cgd force one or the other).
+    const char* fk = getenv("VOID_AMD_KERNEL");
+    const bool pair = fk && (strcmp(fk, "cgdk") == 0 || strcmp(fk, "cgd") == 0)
+                          ? strcmp(fk, "cgdk") == 0
+                          : (n_split_tiles > 0 ? grid < kDeepGridRounds * 1024 : grid <= kPairGridMax);
+    auto go16 = [&](auto elt_c) -> int {
+      constexpr int E = decltype(elt_c)::value;
+      auto pick = [&](auto out_c) -> int {
+        constexpr int O = decltype(out_c)::value;
+        if (pair) return launch_cg<E, VOID_EPI_PER_BLOCK, O, false, true, kDmaTiles, 2>(p, grid, stream);
+        return launch_cg<E, VOID_EPI_PER_BLOCK, O, false, true>(p, grid, stream);
+      };
       switch (d->out_dtype) {
-        case VOID_DT_F32: return launch_cg<kEltBf16, VOID_EPI_PER_BLOCK, VOID_DT_F32, false, true>(p, grid, stream);
-        case VOID_DT_BF16: return launch_cg<kEltBf16, VOID_EPI_PER_BLOCK, VOID_DT_BF16, false, true>(p, grid, stream);
-        case VOID_DT_F16: return launch_cg<kEltBf16, VOID_EPI_PER_BLOCK, VOID_DT_F16, false, true>(p, grid, stream);
-        default: break;
+        case VOID_DT_F32: return pick(std::integral_constant<int, VOID_DT_F32>{});
+        case VOID_DT_BF16: return pick(std::integral_constant<int, VOID_DT_BF16>{});
+        case VOID_DT_F16: return pick(std::integral_constant<int, VOID_DT_F16>{});
+        default: return fail(VOID_ERR_UNSUPPORTED, "16-bit SpMM writes f32, bf16 or f16");
       }
-    } else {
-      switch (d->out_dtype) {
-        case VOID_DT_F32: return launch_cg<kEltF16, VOID_EPI_PER_BLOCK, VOID_DT_F32, false, true>(p, grid, stream);
-        case VOID_DT_BF16: return launch_cg<kEltF16, VOID_EPI_PER_BLOCK, VOID_DT_BF16, false, true>(p, grid, stream);
-        case VOID_DT_F16: return launch_cg<kEltF16, VOID_EPI_PER_BLOCK, VOID_DT_F16, false, true>(p, grid, stream);
-        default: break;
-      }
-    }
-    return fail(VOID_ERR_UNSUPPORTED, "16-bit SpMM writes f32, bf16 or f16");
+    };
+    if (elt == kEltBf16) return go16(std::integral_constant<int, kEltBf16>{});
+    return go16(std::integral_constant<int, kEltF16>{});
   }
   if (elt == kEltF32) {
     const bool vec = c_ok && (bu % 16 == 0) && (d->ldb % 4 == 0) && (d->N % 4 == 0);
