@@ -63,8 +63,8 @@ def parse():
                          "of c2's byte count in the same cold harness")
     ap.add_argument("--epilogue", default=None, help="int8 epilogue (default per_block)")
     ap.add_argument("--dtype", default="f32", choices=["f32", "bf16", "f16"],
-                    help="--op float: tile and B dtype (bf16 / f16 run the 16-bit MFMA kernel, output in the "
-                         "same dtype)")
+                    help="--op float / sddmm: operand dtype (bf16 / f16 run the 16-bit MFMA kernels, output in "
+                         "the same dtype)")
     ap.add_argument("--chunk", type=int, default=None, help="override the Stream-K chunk")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--profile", action="store_true", help="no CPU leg, no flush: for rocprofv3 runs")
@@ -287,26 +287,26 @@ def bench_float(args, dev):
     B = torch.from_numpy(case.b).to(dev)
     dt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[args.dtype]
     esz = 4 if dt == torch.float32 else 2
-    if args.op == "float" and dt != torch.float32:
+    if dt != torch.float32:
         vt, B = vt.to_dtype(dt), B.to(dt)
     nb = vt.n_blocks
     ops = 2.0 * nb * 1024 * case.N
     if args.op == "sddmm":
         from void_amd import _runtime
         from void_amd.format import build_bsr_layout
-        G = torch.randn(case.M, case.N, device=dev)
+        G = torch.randn(case.M, case.N, device=dev).to(dt)
         rows, cols = vt.block_rows.to(torch.int32), vt.block_cols.to(torch.int32)
         # The backward's own path: tiles grouped by block-row (void_sddmm_rows_f32).
         lay = build_bsr_layout(rows, cols, vt.block_grid[0], vt.block_grid[1], dev)
         lay.row_groups()
-        run = lambda: _runtime.sddmm_tiles(G, B, rows, cols, (case.M, case.K), torch.float32, layout=lay)
-        nbytes = nb * (4096 + 8) + 4 * case.M * case.N + 4 * case.K * case.N
+        run = lambda: _runtime.sddmm_tiles(G, B, rows, cols, (case.M, case.K), dt, layout=lay)
+        nbytes = nb * (1024 * esz + 8) + esz * case.M * case.N + esz * case.K * case.N
     else:
         out = torch.empty(case.M, case.N, device=dev, dtype=dt)
         run = lambda: void_amd.void_spmm(vt, B, out=out)
         nbytes = nb * (1024 * esz + 4) + 4 * (vt.block_grid[0] + 1) + esz * case.K * case.N + esz * case.M * case.N
     cold, hot, wall = time_gpu({"run": run}, args.steps, args.warmup, flush=True)
-    peak = FP32_PEAK_TFLOPS if esz == 4 or args.op == "sddmm" else BF16_PEAK_TFLOPS
+    peak = FP32_PEAK_TFLOPS if esz == 4 else BF16_PEAK_TFLOPS
     t_mem, t_ops = nbytes / (HBM_PEAK_GBS * 1e9), ops / (peak * 1e12)
     tflops = ops / (cold * 1e-3) / 1e12
     if t_ops >= t_mem:
@@ -357,8 +357,8 @@ def bench_float(args, dev):
         cpu = {"value": round(ops / med / 1e12, 4), "unit": "TFLOP/s", "cores": len(os.sched_getaffinity(0)),
                "kind": "port", "ms": round(med * 1e3, 3),
                "sample": f"full {args.config} problem in fp32, torch CPU tile bmm + index_add, median of {len(times) - 1} reps"}
-    what = "SDDMM backward of A (void_sddmm_rows_f32)" if args.op == "sddmm" else "BSpMM (void_spmm)"
-    dname = "f32" if args.op == "sddmm" else args.dtype
+    what = f"SDDMM backward of A (void_sddmm_rows_{args.dtype})" if args.op == "sddmm" else "BSpMM (void_spmm)"
+    dname = args.dtype
     line = {"metric": f"{dname.upper()} {what} effective TFLOP/s, {case.name} in {dname}", "value": round(tflops, 3),
             "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(cold, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,

@@ -344,6 +344,19 @@ int void_sddmm_rows_f32(const float* grad_c, int64_t ldg, const float* b, int64_
                         int32_t n_groups, const int32_t* col_idx, const int64_t* tile_index, int32_t M, int32_t N,
                         int32_t K, void* grad_tiles, int32_t out_dtype, hipStream_t stream);
 
+/* void_sddmm_rows_f32 for 16-bit grad_c and b of one dtype (bf16 or fp16),
+ * the backward of a VOID tensor in that dtype: products of the 16-bit values
+ * on the 16-bit MFMA (exact in fp32), fp32 accumulation, written as
+ * out_dtype.  Needs 16-byte aligned operands with ldg, ldb and N multiples
+ * of 8 (else VOID_ERR_UNSUPPORTED).  Replaces void_spmm_backward_a_kernel
+ * (void/autograd.py:14-97), whose tl.dot takes 16-bit operands as they are. */
+int void_sddmm_rows_bf16(const void* grad_c, int64_t ldg, const void* b, int64_t ldb, const int32_t* groups,
+                         int32_t n_groups, const int32_t* col_idx, const int64_t* tile_index, int32_t M, int32_t N,
+                         int32_t K, void* grad_tiles, int32_t out_dtype, hipStream_t stream);
+int void_sddmm_rows_f16(const void* grad_c, int64_t ldg, const void* b, int64_t ldb, const int32_t* groups,
+                        int32_t n_groups, const int32_t* col_idx, const int64_t* tile_index, int32_t M, int32_t N,
+                        int32_t K, void* grad_tiles, int32_t out_dtype, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

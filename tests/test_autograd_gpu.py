@@ -92,6 +92,74 @@ def test_sddmm_tiles_half_outputs(gpu, out_dtype, grouped, monkeypatch):
         bound = N * U * (np.abs(x) @ np.abs(y).T) * (1 + rel) + rel * np.abs(ref) + ab
         assert np.all(np.abs(got[t].float().cpu().numpy() - ref) <= bound + 1e-30), t
 
+@pytest.mark.parametrize("in_dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("same_out", [True, False], ids=["out16", "out32"])
+@pytest.mark.parametrize("M,K,N,n,seed", [(1024, 2048, 512, 600, 0), (100, 70, 40, 6, 1), (64, 96, 136, 5, 2),
+                                          (256, 4096, 72, 300, 3), (96, 128, 1000, 12, 4), (500, 300, 8, 30, 6),
+                                          (70, 1000, 20, 40, 5)])
+def test_sddmm16(gpu, in_dtype, same_out, M, K, N, n, seed):
+    """16-bit grad_c and B of one dtype (the backward of a bf16 / fp16 VOID
+    tensor): void_sddmm_rows_bf16 / _f16 on the 16-bit MFMA when N % 8 == 0
+    (64-column chunks, the last cut by N), the fp32 kernel on widened copies
+    otherwise (N = 20).  Same bound on the 16-bit values as the fp32 path,
+    plus one rounding of a 16-bit output."""
+    from void_amd.format import build_bsr_layout
+    rng = np.random.default_rng(100 + seed)
+    nbr, nbc = -(-M // 32), -(-K // 32)
+    flat = rng.choice(nbr * nbc, min(n, nbr * nbc), replace=False)
+    rows, cols = (flat // nbc).astype(np.int32), (flat % nbc).astype(np.int32)
+    G = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).to(in_dtype)
+    B = torch.from_numpy(rng.standard_normal((K, N)).astype(np.float32)).to(in_dtype)
+    tr, tc = torch.from_numpy(rows).to(gpu), torch.from_numpy(cols).to(gpu)
+    lay = build_bsr_layout(tr, tc, nbr, nbc, gpu)
+    out_dtype = in_dtype if same_out else torch.float32
+    got = _runtime.sddmm_tiles(G.to(gpu), B.to(gpu), tr, tc, (M, K), out_dtype, layout=lay)
+    assert got.dtype == out_dtype
+    rel, ab = _HALF[out_dtype] if same_out else (0.0, 0.0)
+    Gp = np.zeros((nbr * 32, N)); Gp[:M] = G.double().numpy()
+    Bp = np.zeros((nbc * 32, N)); Bp[:K] = B.double().numpy()
+    for t in range(len(rows)):
+        x, y = Gp[rows[t] * 32:(rows[t] + 1) * 32], Bp[cols[t] * 32:(cols[t] + 1) * 32]
+        ref = x @ y.T
+        bound = N * U * (np.abs(x) @ np.abs(y).T) * (1 + rel) + rel * np.abs(ref) + ab
+        assert np.all(np.abs(got[t].float().cpu().numpy() - ref) <= bound + 1e-30), t
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_voidspmm_gradients_16bit(gpu, dtype):
+    """A bf16 / fp16 VOID tensor times an input of the same dtype: forward
+    and the product for the input's gradient on the 16-bit SpMM, the tiles'
+    gradient on the 16-bit SDDMM, each within the fp32 summation bound on the
+    16-bit values plus one rounding of the 16-bit result."""
+    case = cases.uniform_blocks(512, 1024, 96, 150, seed=5)
+    vt = cases.make_void_tensor(case, "cpu").to_dtype(dtype).to(gpu)
+    mod = void_amd.VOIDSpMM(vt).to(gpu)
+    x = torch.randn(1024, 96, device=gpu).to(dtype).requires_grad_(True)
+    w = torch.randn(512, 96, device=gpu).to(dtype)
+    y = mod(x)
+    assert y.dtype == dtype
+    (y * w).sum().backward()
+    rel, ab = _HALF[dtype]
+    A = oracle.densify(vt.values.float().cpu().numpy(), case.block_rows, case.block_cols, (512, 1024)).astype(np.float64)
+    X, W = x.detach().double().cpu().numpy(), w.double().cpu().numpy()
+    n_row = np.bincount(case.block_rows, minlength=16).max()
+    ref = A @ X
+    assert np.all(np.abs(y.detach().double().cpu().numpy() - ref) <=
+                  32 * n_row * U * (np.abs(A) @ np.abs(X)) + rel * np.abs(ref) + ab + 1e-30)
+    gX = A.T @ W
+    n_col = np.bincount(case.block_cols, minlength=32).max()
+    assert np.all(np.abs(x.grad.double().cpu().numpy() - gX) <=
+                  32 * n_col * U * (np.abs(A).T @ np.abs(W)) + rel * np.abs(gX) + ab + 1e-30)
+    gA = W @ X.T
+    tiles = mod.values.grad.double().cpu().numpy()
+    bound_full = 96 * U * (np.abs(W) @ np.abs(X).T)
+    rr, cc = vt.block_rows.cpu().numpy(), vt.block_cols.cpu().numpy()
+    for t in range(len(tiles)):
+        r, c = rr[t] * 32, cc[t] * 32
+        g = gA[r:r + 32, c:c + 32]
+        assert np.all(np.abs(tiles[t] - g) <= bound_full[r:r + 32, c:c + 32] + rel * np.abs(g) + ab + 1e-30)
+
+
 def test_voidspmm_gradients(gpu):
     case = cases.uniform_blocks(512, 1024, 96, 150, seed=5)
     vt = cases.make_void_tensor(case, "cpu").to(gpu)

@@ -137,6 +137,10 @@ SIGNATURES = {
                                c_int32, c_int32, c_void_p, c_int32, c_void_p]),
     "void_sddmm_rows_f32": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int32, c_void_p, c_void_p,
                                     c_int32, c_int32, c_int32, c_void_p, c_int32, c_void_p]),
+    "void_sddmm_rows_bf16": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int32, c_void_p, c_void_p,
+                                     c_int32, c_int32, c_int32, c_void_p, c_int32, c_void_p]),
+    "void_sddmm_rows_f16": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int32, c_void_p, c_void_p,
+                                    c_int32, c_int32, c_int32, c_void_p, c_int32, c_void_p]),
     "void_csr_workspace_bytes": (c_size_t, [c_int32, c_int32]),
     "void_csr_count_blocks": (c_int, [c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_size_t, c_void_p,
                                       c_void_p]),

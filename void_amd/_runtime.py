@@ -472,7 +472,8 @@ def sddmm_tiles(grad_c: torch.Tensor, b: torch.Tensor, block_rows: torch.Tensor,
 
     With the tiles' BsrLayout (block-row order and the Morton index of each
     position), void_sddmm_rows_f32 shares each block-row's grad_c rows among
-    its tiles; without it, void_sddmm_f32 takes the tiles one by one."""
+    its tiles (void_sddmm_rows_bf16 / _f16 when grad_c and b share a 16-bit
+    dtype); without it, void_sddmm_f32 takes the tiles one by one."""
     M, K = shape
     n = int(block_rows.numel())
     N = grad_c.shape[1]
@@ -481,9 +482,23 @@ def sddmm_tiles(grad_c: torch.Tensor, b: torch.Tensor, block_rows: torch.Tensor,
         return out
     if N == 0:
         return out.zero_()
+    stream = torch.cuda.current_stream(grad_c.device).cuda_stream
+    entry16 = {torch.bfloat16: "void_sddmm_rows_bf16", torch.float16: "void_sddmm_rows_f16"}.get(grad_c.dtype)
+    if layout is not None and entry16 is not None and b.dtype == grad_c.dtype:
+        # 16-bit operands of one dtype on the 16-bit MFMA (16-byte rows).
+        g16 = grad_c if grad_c.stride(1) == 1 else grad_c.contiguous()
+        b16 = b if b.stride(1) == 1 else b.contiguous()
+        if (N % 8 == 0 and g16.stride(0) % 8 == 0 and b16.stride(0) % 8 == 0 and g16.data_ptr() % 16 == 0
+                and b16.data_ptr() % 16 == 0 and 32 * max(g16.stride(0), b16.stride(0)) * 2 < (1 << 31)):
+            groups = layout.row_groups()
+            st = getattr(_lib.lib(), entry16)(g16.data_ptr(), g16.stride(0), b16.data_ptr(), b16.stride(0),
+                                              groups.data_ptr(), int(groups.shape[0]), layout.col_idx.data_ptr(),
+                                              layout.order.data_ptr(), M, N, K, out.data_ptr(), out_code(out_dtype),
+                                              stream)
+            _lib.check(st, entry16)
+            return out
     g = grad_c.to(torch.float32).contiguous()
     bb = b.to(torch.float32).contiguous()
-    stream = torch.cuda.current_stream(g.device).cuda_stream
     if layout is not None:
         groups = layout.row_groups()
         st = _lib.lib().void_sddmm_rows_f32(g.data_ptr(), g.stride(0), bb.data_ptr(), bb.stride(0), groups.data_ptr(),

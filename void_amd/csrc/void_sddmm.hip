@@ -35,6 +35,8 @@ constexpr int kWaves = 4;  // waves per tile, each a quarter of the chunks of N
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8hf __attribute__((ext_vector_type(8)));
 
 struct Chunk {
   v4f x[4];  // dC[row_x][n0 + 16g + 4q .. +3]
@@ -303,14 +305,23 @@ struct RingGeo {
 // of workgroup b with a dC block of its own; a stage holds each wave's dC
 // and B blocks of a 16-column chunk (32 KB, 64 KB double-buffered, two
 // workgroups per CU), 4 loads per wave.
-template <int OUT, bool PER_TILE>
+//
+// IN = VOID_DT_BF16 / VOID_DT_F16 (void_sddmm_rows_bf16 / _f16): 16-bit dC and
+// B with the same byte geometry, so a chunk holds twice the columns; lane
+// (i, g) feeds v_mfma_f32_32x32x16_{bf16,f16} q with its q-th 16-byte segment
+// (8 consecutive n) of row i of both operands, whose products are exact in
+// fp32 as on the fp32 MFMA.
+template <int OUT, bool PER_TILE, int IN = VOID_DT_F32>
 __global__ __launch_bounds__(64 * kRW) void sddmm_ring_kernel(
-    const float* __restrict__ dC, int64_t ldg, const float* __restrict__ B, int64_t ldb,
+    const void* __restrict__ dC, int64_t ldg, const void* __restrict__ B, int64_t ldb,
     const int32_t* __restrict__ groups, const int32_t* __restrict__ col_idx, const int64_t* __restrict__ tile_index,
     const int32_t* __restrict__ block_rows, const int32_t* __restrict__ block_cols, int32_t n_blocks,
     int32_t M, int32_t N, int32_t K, void* __restrict__ grad) {
-  constexpr int kCW = PER_TILE ? 16 : 32;  // columns of N per chunk
-  using Geo = RingGeo<kCW>;
+  constexpr int kEsz = IN == VOID_DT_F32 ? 4 : 2;
+  constexpr int kCW4 = PER_TILE ? 16 : 32;  // chunk width in 4-byte words
+  constexpr int kCW = kCW4 * 4 / kEsz;      // columns of N per chunk
+  constexpr int kEps = 16 / kEsz;           // columns per 16-byte segment
+  using Geo = RingGeo<kCW4>;
   constexpr int kSegs = Geo::kSegs, kRowsPerLoad = Geo::kRowsPerLoad, kLoadsPerBlk = Geo::kLoadsPerBlk;
   constexpr int kBlk = Geo::kBlk;
   constexpr int kStage = PER_TILE ? 2 * kRW * kBlk : (1 + kRW) * kBlk;
@@ -347,7 +358,8 @@ __global__ __launch_bounds__(64 * kRW) void sddmm_ring_kernel(
   // l % kSegs holding source segment (l % kSegs) ^ swz(row).  Rows past M
   // (dC) or K (B), and segments past N (N is a multiple of 4 here), read
   // zeros.
-  const v4s rx = sgpr_rsrc(dC + (int64_t)br * kT * ldg), ry = sgpr_rsrc(B + (int64_t)bc * kT * ldb);
+  const v4s rx = sgpr_rsrc(static_cast<const char*>(dC) + (int64_t)br * kT * ldg * kEsz),
+            ry = sgpr_rsrc(static_cast<const char*>(B) + (int64_t)bc * kT * ldb * kEsz);
   int vy[kLoadsPerBlk], vx[kLoadsPerBlk], sg[kLoadsPerBlk];
 #pragma unroll
   for (int h = 0; h < kLoadsPerBlk; ++h) {
@@ -356,26 +368,27 @@ __global__ __launch_bounds__(64 * kRW) void sddmm_ring_kernel(
     const int row = kRowsPerLoad * h + lane / kSegs;
     const int xrow = kRowsPerLoad * hx + lane / kSegs;
     sg[h] = (lane % kSegs) ^ Geo::swz(row);
-    vy[h] = has && bc * kT + row < K ? row * (int)ldb * 4 + sg[h] * 16 : kOutOfRange;
+    vy[h] = has && bc * kT + row < K ? row * (int)ldb * kEsz + sg[h] * 16 : kOutOfRange;
     const bool x_live = PER_TILE ? has : wave < kLoadsPerBlk;
-    vx[h] = x_live && br * kT + xrow < M ? xrow * (int)ldg * 4 + ((lane % kSegs) ^ Geo::swz(xrow)) * 16 : kOutOfRange;
+    vx[h] = x_live && br * kT + xrow < M ? xrow * (int)ldg * kEsz + ((lane % kSegs) ^ Geo::swz(xrow)) * 16 : kOutOfRange;
   }
   auto issue = [&](int ch) {
     uint8_t* st = smem + (ch % kRing) * kStage;
     const int n0 = ch * kCW;
 #pragma unroll
     for (int h = 0; h < kLoadsPerBlk; ++h)
-      dma_b128(ry, st + yoff + h * 1024, n0 + 4 * sg[h] < N ? vy[h] : kOutOfRange, n0 * 4);
+      dma_b128(ry, st + yoff + h * 1024, n0 + kEps * sg[h] < N ? vy[h] : kOutOfRange, n0 * kEsz);
     if constexpr (PER_TILE) {
 #pragma unroll
       for (int h = 0; h < kLoadsPerBlk; ++h)
-        dma_b128(rx, st + xoff + h * 1024, n0 + 4 * sg[h] < N ? vx[h] : kOutOfRange, n0 * 4);
+        dma_b128(rx, st + xoff + h * 1024, n0 + kEps * sg[h] < N ? vx[h] : kOutOfRange, n0 * kEsz);
     } else {
       // The dC part's rows lie whole 8-row groups from part 0's, and with 8
       // segments per row the swizzle depends only on the row mod 8, so
       // sg[0] is this lane's dC segment too.
       const bool x_wave = wave < kLoadsPerBlk;
-      dma_b128(rx, x_wave ? st + wave * 1024 : smem + kRingJunk, n0 + 4 * sg[0] < N ? vx[0] : kOutOfRange, n0 * 4);
+      dma_b128(rx, x_wave ? st + wave * 1024 : smem + kRingJunk, n0 + kEps * sg[0] < N ? vx[0] : kOutOfRange,
+               n0 * kEsz);
     }
   };
 
@@ -383,7 +396,7 @@ __global__ __launch_bounds__(64 * kRW) void sddmm_ring_kernel(
   constexpr int kHalf = kSegs / 2;
   int rd[kHalf];
 #pragma unroll
-  for (int q = 0; q < kHalf; ++q) rd[q] = i * (kCW * 4) + (((kHalf * g + q) ^ Geo::swz(i)) << 4);
+  for (int q = 0; q < kHalf; ++q) rd[q] = i * (kCW4 * 4) + (((kHalf * g + q) ^ Geo::swz(i)) << 4);
   v16f acc = {};
 #pragma unroll
   for (int k = 0; k < kRing - 1; ++k)
@@ -402,10 +415,22 @@ __global__ __launch_bounds__(64 * kRW) void sddmm_ring_kernel(
         x[q] = *reinterpret_cast<const v4f*>(st + xoff + rd[q]);
         y[q] = *reinterpret_cast<const v4f*>(st + yoff + rd[q]);
       }
+      if constexpr (IN == VOID_DT_F32) {
 #pragma unroll
-      for (int q = 0; q < kHalf; ++q)
+        for (int q = 0; q < kHalf; ++q)
 #pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x[q][s2], y[q][s2], acc, 0, 0, 0);
+          for (int s2 = 0; s2 < 4; ++s2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x[q][s2], y[q][s2], acc, 0, 0, 0);
+      } else if constexpr (IN == VOID_DT_BF16) {
+#pragma unroll
+        for (int q = 0; q < kHalf; ++q)
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, x[q]), __builtin_bit_cast(v8bf, y[q]),
+                                                        acc, 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int q = 0; q < kHalf; ++q)
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8hf, x[q]), __builtin_bit_cast(v8hf, y[q]),
+                                                       acc, 0, 0, 0);
+      }
     }
   }
   if (!has) return;
@@ -463,7 +488,64 @@ int go_rows(const float* dC, int64_t ldg, const float* B, int64_t ldb, const int
   return VOID_OK;
 }
 
+// 16-bit operands: the row-grouped ring only (16-byte aligned rows, N % 8
+// == 0, 31-bit offsets within 32 rows of either operand).
+template <int IN>
+int go_rows16(const void* dC, int64_t ldg, const void* B, int64_t ldb, const int32_t* groups, int32_t n_groups,
+              const int32_t* col_idx, const int64_t* tile_index, int32_t M, int32_t N, int32_t K, void* grad,
+              int32_t out_dtype, hipStream_t stream) {
+  const bool ok = ((uintptr_t)dC % 16 == 0) && ((uintptr_t)B % 16 == 0) && ldg % 8 == 0 && ldb % 8 == 0 &&
+                  N % 8 == 0 && (int64_t)kT * ldg * 2 < INT32_MAX && (int64_t)kT * ldb * 2 < INT32_MAX;
+  if (!ok)
+    return void_internal_fail(VOID_ERR_UNSUPPORTED,
+                              "16-bit SDDMM needs 16-byte aligned rows (ldg, ldb, N multiples of 8)");
+  auto launch = [&](auto k) {
+    hipLaunchKernelGGL(k, dim3(n_groups), dim3(64 * kRW), 0, stream, dC, ldg, B, ldb, groups, col_idx, tile_index,
+                       nullptr, nullptr, 0, M, N, K, grad);
+  };
+  switch (out_dtype) {
+    case VOID_DT_F32: launch(sddmm_ring_kernel<VOID_DT_F32, false, IN>); break;
+    case VOID_DT_BF16: launch(sddmm_ring_kernel<VOID_DT_BF16, false, IN>); break;
+    case VOID_DT_F16: launch(sddmm_ring_kernel<VOID_DT_F16, false, IN>); break;
+    default: return void_internal_fail(VOID_ERR_UNSUPPORTED, "gradient tiles are f32, bf16 or f16");
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return void_internal_fail(VOID_ERR_HIP, hipGetErrorString(e));
+  return VOID_OK;
+}
+
+int rows16_args(const void* grad_c, int64_t ldg, const void* b, int64_t ldb, const int32_t* groups, int32_t n_groups,
+                const int32_t* col_idx, int32_t M, int32_t N, int32_t K, void* grad_tiles) {
+  void_internal_fail(VOID_OK, "");
+  if (n_groups < 0 || M < 0 || N < 0 || K < 0) return void_internal_fail(VOID_ERR_ARG, "negative size");
+  if (n_groups == 0) return VOID_OK;
+  if (!grad_c || !b || !groups || !col_idx || !grad_tiles) return void_internal_fail(VOID_ERR_ARG, "null pointer");
+  if (ldg < N || ldb < N) return void_internal_fail(VOID_ERR_ARG, "leading dimension smaller than N");
+  if (N == 0) return void_internal_fail(VOID_ERR_ARG, "N = 0: the gradient is zero, fill it instead");
+  return VOID_OK;
+}
+
 }  // namespace
+
+extern "C" int void_sddmm_rows_bf16(const void* grad_c, int64_t ldg, const void* b, int64_t ldb,
+                                    const int32_t* groups, int32_t n_groups, const int32_t* col_idx,
+                                    const int64_t* tile_index, int32_t M, int32_t N, int32_t K, void* grad_tiles,
+                                    int32_t out_dtype, hipStream_t stream) {
+  const int st = rows16_args(grad_c, ldg, b, ldb, groups, n_groups, col_idx, M, N, K, grad_tiles);
+  if (st != VOID_OK || n_groups == 0) return st;
+  return go_rows16<VOID_DT_BF16>(grad_c, ldg, b, ldb, groups, n_groups, col_idx, tile_index, M, N, K, grad_tiles,
+                                 out_dtype, stream);
+}
+
+extern "C" int void_sddmm_rows_f16(const void* grad_c, int64_t ldg, const void* b, int64_t ldb,
+                                   const int32_t* groups, int32_t n_groups, const int32_t* col_idx,
+                                   const int64_t* tile_index, int32_t M, int32_t N, int32_t K, void* grad_tiles,
+                                   int32_t out_dtype, hipStream_t stream) {
+  const int st = rows16_args(grad_c, ldg, b, ldb, groups, n_groups, col_idx, M, N, K, grad_tiles);
+  if (st != VOID_OK || n_groups == 0) return st;
+  return go_rows16<VOID_DT_F16>(grad_c, ldg, b, ldb, groups, n_groups, col_idx, tile_index, M, N, K, grad_tiles,
+                                out_dtype, stream);
+}
 
 extern "C" int void_sddmm_f32(const float* grad_c, int64_t ldg, const float* b, int64_t ldb,
                               const int32_t* block_rows, const int32_t* block_cols, int32_t n_blocks, int32_t M,
