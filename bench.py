@@ -51,8 +51,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default=None, choices=["c1", "c2", "c3", "c3f", "c4", "c5"],
-                    help="workload (default c2, the headline; c3f is config 3 with B kept in fp32)")
+    ap.add_argument("--config", default=None, choices=["c1", "c2", "c3", "c3f", "c3h", "c4", "c5"],
+                    help="workload (default c2, the headline; c3f / c3h are config 3 with B kept in fp32 / bf16)")
     ap.add_argument("--no-per-config", dest="per_config", action="store_false",
                     help="the default run skips the other configs' extra.per_config entries")
     ap.add_argument("--op", default="spmm", choices=["spmm", "quantize", "format", "float", "sddmm", "floor"],
@@ -79,7 +79,8 @@ def build_problem(cfg: str, dev, epilogue):
     quantisers (on the host, outside every timed region), and the SpMM call.
 
     cfg: c1..c5 as BASELINE.json lists them; c3f is config 3's A with B kept
-    in fp32, the reference's default FP8 call (float B, fp16 output)."""
+    in fp32, the reference's default FP8 call (float B, fp16 output); c3h the
+    same call with B in bf16."""
     import torch
 
     import cases
@@ -93,7 +94,7 @@ def build_problem(cfg: str, dev, epilogue):
         case = cases.BlockCase("c1_plumbing_512_n128", 512, 512, 128, vt.values.numpy(),
                                vt.block_rows.numpy(), vt.block_cols.numpy(), B)
     else:
-        gen = {"c2": cases.c2_int8, "c3": cases.c3_fp8, "c3f": cases.c3_fp8, "c4": cases.c4_powerlaw,
+        gen = {"c2": cases.c2_int8, "c3": cases.c3_fp8, "c3f": cases.c3_fp8, "c3h": cases.c3_fp8, "c4": cases.c4_powerlaw,
                "c5": cases.c5_ffn}[cfg]
         case = gen()
         vt = cases.make_void_tensor(case, "cpu")
@@ -117,6 +118,20 @@ def build_problem(cfg: str, dev, epilogue):
         a_scales = f8.scaling_info.scale.cpu().numpy()
         tiles_f = f8.values_fp8.float().cpu()
         b_deq = torch.from_numpy(case.b)
+    elif cfg == "c3h":
+        f8 = void_amd.void_tensor_to_fp8(vt).to(dev)
+        bt = torch.from_numpy(case.b).to(torch.bfloat16).to(dev)
+        out = torch.empty(M, N, dtype=torch.float16, device=dev)
+
+        def run():
+            return void_amd.void_spmm_fp8(f8, bt, output_dtype=torch.float16, out=out)
+
+        prob.update(kind="fp8", dtype="fp8e4m3 x bf16", out_bytes=2, b_scale_bytes=0, run=run,
+                    peak_ops=BF16_PEAK_TFLOPS, epilogue="per_block", b_bytes=2 * K * N,
+                    workload=case.name.replace("c3_fp8", "c3h_fp8_bf16_b"))
+        a_scales = f8.scaling_info.scale.cpu().numpy()
+        tiles_f = f8.values_fp8.float().cpu()
+        b_deq = bt.float().cpu()
     elif cfg == "c3":
         f8 = void_amd.void_tensor_to_fp8(vt).to(dev)
         bq, bs = quantize_dense_fp8(torch.from_numpy(case.b))
@@ -505,8 +520,8 @@ def cpu_leg(prob, budget_s: float, cfg: str) -> dict:
 
 # Configs reported next to the headline (BASELINE.json asks for every one):
 # c1, c3 as configured (E4M3 B, bf16 out), c3f (the reference's default FP8
-# call: float B, fp16 out), c4 and c5.
-PER_CONFIG = ("c1", "c3", "c3f", "c4", "c5")
+# call: float B, fp16 out), c3h (the same with a bf16 B), c4 and c5.
+PER_CONFIG = ("c1", "c3", "c3f", "c3h", "c4", "c5")
 
 
 def per_config_line(cfg: str, dev, args) -> dict:

@@ -256,6 +256,16 @@ int void_spmm_fp8(const void_bsr_desc* a, const void_dense_args* d, const void_p
 int void_spmm_fp8_f32b(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
                        void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* The same for a 16-bit B: d->b holds bf16 (b_dtype VOID_DT_BF16) or fp16
+ * (VOID_DT_F16) values, which the reference's upcast (void/fp8.py:624-671)
+ * takes as they are.  The E4M3 tiles are decoded exactly to B's type and
+ * multiplied on the 16-bit MFMA (exact products, fp32 accumulation), each
+ * tile's product scaled into the sum.  B and C row-major with 16-byte
+ * aligned rows and N % 8 == 0 (else VOID_ERR_UNSUPPORTED); plan items of at
+ * most 64 tiles. */
+int void_spmm_fp8_b16(const void_bsr_desc* a, const void_dense_args* d, int32_t b_dtype, const void_plan* plan,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* Float SpMM: fp32 tiles times fp32 B on the fp32 MFMA (exact products,
  * fp32 accumulation), then bias, activation and conversion to d->out_dtype
  * (f32, bf16 or f16).  Replaces void_spmm_kernel + void_spmm

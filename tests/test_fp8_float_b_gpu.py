@@ -128,3 +128,87 @@ def test_fp8_float_b_differs_from_quantised_b(gpu):
     e_gpu = np.abs(out.cpu().numpy() - ref).max()
     e_q = np.abs(quantised - ref).max()
     assert e_gpu < e_q / 100, (e_gpu, e_q)
+
+
+# A 16-bit B (void_spmm_fp8_b16): the E4M3 codes decoded exactly to B's type
+# on the 16-bit MFMA, exact products; the same bar as the fp32 B.
+_B16 = [torch.bfloat16, torch.float16]
+
+
+@pytest.fixture(params=["default", "cgd", "cgdk"])
+def ring(request, monkeypatch):
+    if request.param == "default":
+        monkeypatch.delenv("VOID_AMD_KERNEL", raising=False)
+    else:
+        monkeypatch.setenv("VOID_AMD_KERNEL", request.param)
+    return request.param
+
+
+def _b16_ref(A, Aabs, b16, sb=1.0):
+    bf = b16.float().numpy()
+    return oracle.fp8_spmm_float_b(A, bf, sb), oracle.fp8_spmm_float_b(Aabs, np.abs(bf), sb)
+
+
+@pytest.mark.parametrize("b_dtype", _B16, ids=["bf16b", "f16b"])
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32], ids=["f16", "bf16", "f32"])
+def test_c3_fp8_b16_full(gpu, b_dtype, out_dtype):
+    """Config 3's A times its B in bf16 / fp16, taken as it is."""
+    key = ("b16", b_dtype)
+    if key not in _C3:
+        case = cases.c3_fp8()
+        f8, A, Aabs = _setup(case)
+        b16 = torch.from_numpy(case.b).to(b_dtype)
+        _C3[key] = (case, f8, b16) + _b16_ref(A, Aabs, b16)
+    case, f8, b16, ref, bound = _C3[key]
+    out = void_amd.void_spmm_fp8(f8.to(gpu), b16.to(gpu), output_dtype=out_dtype)
+    assert out.dtype == out_dtype
+    _check(out.float().cpu().numpy(), ref, bound, out_dtype)
+
+
+@pytest.mark.parametrize("b_dtype", _B16, ids=["bf16b", "f16b"])
+@pytest.mark.parametrize("M,K,N", [(333, 555, 64), (100, 70, 40), (64, 200, 136), (1000, 96, 264), (70, 40, 36),
+                                   (96, 64, 13)])
+def test_fp8_b16_ragged(gpu, ring, b_dtype, M, K, N):
+    """Ragged M and K (a last B slab crossing K loads no rows past K); N not
+    a multiple of 8 takes the widened fp32 route, with the same bar."""
+    case = cases.uniform_blocks(M, K, N, max(1, (-(-M // 32)) * (-(-K // 32)) // 3), seed=M + N)
+    f8, A, Aabs = _setup(case)
+    b16 = torch.from_numpy(case.b).to(b_dtype)
+    out = void_amd.void_spmm_fp8(f8.to(gpu), b16.to(gpu), output_dtype=torch.float32)
+    _check(out.cpu().numpy(), *_b16_ref(A, Aabs, b16), torch.float32)
+
+
+@pytest.mark.parametrize("chunk", [1, 3, 7])
+def test_fp8_b16_split_rows(gpu, ring, chunk):
+    """Forced Stream-K splits with a bf16 B: deterministic fix-up."""
+    case = cases.uniform_blocks(1024, 2048, 256, 900, seed=3)
+    f8, A, Aabs = _setup(case)
+    b16 = torch.from_numpy(case.b).to(torch.bfloat16)
+    b = b16.to(gpu)
+    out = void_amd.void_spmm_fp8(f8.to(gpu), b, output_dtype=torch.float32, chunk_tiles=chunk)
+    again = void_amd.void_spmm_fp8(f8.to(gpu), b, output_dtype=torch.float32, chunk_tiles=chunk)
+    assert torch.equal(out.view(torch.int32), again.view(torch.int32))
+    _check(out.cpu().numpy(), *_b16_ref(A, Aabs, b16), torch.float32)
+
+
+@pytest.mark.parametrize("b_dtype", _B16, ids=["bf16b", "f16b"])
+def test_fp8_b16_scales_bias_gelu_strided(gpu, b_dtype):
+    """Per-column b_scale, bias and GELU into a bf16 output that is a column
+    slice of a wider buffer, B a column slice of a wider matrix."""
+    case = cases.uniform_blocks(256, 512, 192, 60, seed=11)
+    f8, A, Aabs = _setup(case)
+    rng = np.random.default_rng(2)
+    sb = rng.uniform(0.5, 2.0, 192).astype(np.float32)
+    bias = rng.standard_normal(192).astype(np.float32)
+    wide = torch.zeros(512, 256, dtype=b_dtype, device=gpu)
+    wide[:, 32:224] = torch.from_numpy(case.b).to(b_dtype).to(gpu)
+    outbuf = torch.zeros(256, 320, dtype=torch.bfloat16, device=gpu)
+    out = outbuf[:, 64:256]
+    void_amd.void_spmm_fp8(f8.to(gpu), wide[:, 32:224], output_dtype=torch.bfloat16, activation="gelu",
+                           bias=torch.from_numpy(bias).to(gpu), b_scale=torch.from_numpy(sb).to(gpu), out=out)
+    b16 = wide[:, 32:224].cpu()
+    pre, bound = _b16_ref(A, Aabs, b16, sb)
+    ref = oracle.gelu_tanh(pre + bias[None, :].astype(np.float64))
+    err = np.abs(out.float().cpu().numpy() - ref)
+    assert np.all(err <= 1.13 * FP8_TOL * bound + 2.0 ** -8 * np.abs(ref) + 1e-4), err.max()
+    assert torch.count_nonzero(outbuf[:, :64]) == 0 and torch.count_nonzero(outbuf[:, 256:]) == 0

@@ -125,6 +125,8 @@ SIGNATURES = {
                               c_void_p, c_size_t, c_void_p]),
     "void_spmm_fp8_f32b": (c_int, [POINTER(BsrDesc), POINTER(DenseArgs), POINTER(Plan),
                                    c_void_p, c_size_t, c_void_p]),
+    "void_spmm_fp8_b16": (c_int, [POINTER(BsrDesc), POINTER(DenseArgs), c_int32, POINTER(Plan),
+                                  c_void_p, c_size_t, c_void_p]),
     "void_spmm_f32": (c_int, [POINTER(BsrDesc), POINTER(DenseArgs), POINTER(Plan),
                               c_void_p, c_size_t, c_void_p]),
     "void_spmm_bf16": (c_int, [POINTER(BsrDesc), POINTER(DenseArgs), POINTER(Plan),

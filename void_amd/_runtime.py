@@ -390,6 +390,10 @@ def launch(kind: str, dbsr: DeviceBsr, b: torch.Tensor, *, b_scale: float = 1.0,
     elif kind == "fp8_f32b":
         st = lib.void_spmm_fp8_f32b(ctypes.byref(desc), ctypes.byref(dense), ctypes.byref(cplan),
                                     ws_ptr, ws_bytes, stream)
+    elif kind in ("fp8_bf16b", "fp8_f16b"):
+        bdt = _lib.DT_BF16 if kind == "fp8_bf16b" else _lib.DT_F16
+        st = lib.void_spmm_fp8_b16(ctypes.byref(desc), ctypes.byref(dense), bdt, ctypes.byref(cplan),
+                                   ws_ptr, ws_bytes, stream)
     else:
         raise ValueError(f"unknown SpMM kind {kind!r}")
     _lib.check(st, f"void_spmm_{kind}")

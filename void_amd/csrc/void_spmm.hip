@@ -67,8 +67,11 @@ typedef float v2f __attribute__((ext_vector_type(2)));
 // Tile element types: int8 and E4M3 tiles times a B of the same type; fp32
 // tiles times fp32 B (float SpMM); E4M3 tiles times fp32 B (kEltFp8F32, the
 // reference's FP8 SpMM with a float B); bf16 or fp16 tiles times a B of the
-// same type (float SpMM on 16-bit tensors, on the 16-bit MFMA).
-enum Elt { kEltI8 = 0, kEltFp8 = 1, kEltF32 = 2, kEltFp8F32 = 3, kEltBf16 = 4, kEltF16 = 5 };
+// same type (float SpMM on 16-bit tensors, on the 16-bit MFMA); E4M3 tiles
+// times a bf16 or fp16 B (the reference's FP8 SpMM with a 16-bit B, on the
+// 16-bit MFMA with A decoded exactly).
+enum Elt { kEltI8 = 0, kEltFp8 = 1, kEltF32 = 2, kEltFp8F32 = 3, kEltBf16 = 4, kEltF16 = 5, kEltFp8Bf16 = 6,
+           kEltFp8F16 = 7 };
 
 struct Params {
   const uint8_t* tiles;
@@ -1032,6 +1035,11 @@ template <int EPI>
 struct Accum1<kEltBf16, EPI> : Accum1<kEltF32, EPI> {};
 template <int EPI>
 struct Accum1<kEltF16, EPI> : Accum1<kEltF32, EPI> {};
+// E4M3 tiles times a 16-bit B: as E4M3 times fp32 B.
+template <int EPI>
+struct Accum1<kEltFp8Bf16, EPI> : Accum1<kEltF32, EPI> {};
+template <int EPI>
+struct Accum1<kEltFp8F16, EPI> : Accum1<kEltF32, EPI> {};
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef _Float16 v8hf __attribute__((ext_vector_type(8)));
@@ -1057,6 +1065,15 @@ __device__ __forceinline__ void e4m3x4_to_bf16(uint32_t w, uint32_t& lo, uint32_
   const v2f f23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
   lo = pack_bf16_trunc(f01[0], f01[1]);
   hi = pack_bf16_trunc(f23[0], f23[1]);
+}
+
+// The same to fp16 (also exact: E4M3's values, subnormals included, lie in
+// fp16's normal range with at most 4 significant bits).
+__device__ __forceinline__ void e4m3x4_to_f16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  const v2f f01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  const v2f f23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f01[0], f01[1]));
+  hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f23[0], f23[1]));
 }
 
 // Split of fp32 x into bf16 hi + lo: hi = x truncated to bf16 (x - hi is then
@@ -1116,22 +1133,24 @@ template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false, int RT = kDmaT
 __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     DMA ? (KS > 1 ? 4 : dma_waves_per_eu(RT)) : 2, DMA ? (KS > 1 ? 4 : dma_waves_per_eu(RT)) : 2))) void spmm_cg_kernel(Params p) {
   static_assert(!(DMA && BCOL), "the LDS-DMA ring is for row-major B");
-  static_assert(KS == 1 || (DMA && (ELT == kEltI8 || ELT == kEltFp8 || ELT == kEltBf16 || ELT == kEltF16) && KS == 2),
-                "the two-ring split is for int8 / fp8 / 16-bit tiles on the LDS-DMA ring");
+  static_assert(KS == 1 || (DMA && ELT != kEltF32 && ELT != kEltFp8F32 && KS == 2),
+                "the two-ring split is for int8 / fp8 / 16-bit B on the LDS-DMA ring");
   using A = Accum1<ELT, EPI>;
   constexpr bool kInt = A::kInt;
   constexpr bool kF32 = ELT == kEltF32;                     // fp32 A tiles
   constexpr bool kBF32 = kF32 || ELT == kEltFp8F32;         // fp32 B slabs
   constexpr bool k16 = ELT == kEltBf16 || ELT == kEltF16;   // 16-bit tiles and B
+  constexpr bool kF8B16 = ELT == kEltFp8Bf16 || ELT == kEltFp8F16;  // E4M3 tiles, 16-bit B
+  constexpr bool kB16 = k16 || kF8B16;                      // 16-bit B slabs
   constexpr bool kFloat = kF32 || k16;                      // unscaled float tiles
-  static_assert(!(kBF32 || k16) || DMA, "fp32 and 16-bit B only on the LDS-DMA ring");
+  static_assert(!(kBF32 || kB16) || DMA, "fp32 and 16-bit B only on the LDS-DMA ring");
   constexpr bool kScales = (EPI == VOID_EPI_PER_BLOCK) && !kFloat;
   // fp32 B: 4 bytes per element, one tile per stage (a 16 KB B slab, and 4 KB
   // of A for fp32 tiles or 1 KB for E4M3 ones); 16-bit: two tiles per stage
   // (8 KB slab + 2 KB tile each).  Either way the ring keeps its 40 KB.
   constexpr int kEsz = kF32 ? 4 : k16 ? 2 : 1;    // A
-  constexpr int kBEsz = kBF32 ? 4 : k16 ? 2 : 1;  // B
-  constexpr int kStageTiles = kBF32 ? 1 : k16 ? 2 : RT;
+  constexpr int kBEsz = kBF32 ? 4 : kB16 ? 2 : 1;  // B
+  constexpr int kStageTiles = kBF32 ? 1 : kB16 ? 2 : RT;
 
   // Tile slots: two batches of the register-staged loop, or the LDS-DMA ring.
   // KS = 2: two groups of 4 waves, each with its own ring, take alternate
@@ -1338,7 +1357,7 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     // q of row r holds global chunk q ^ ((r >> 2) & 3).
     int voffs_h[2] = {0, 0}, voffs_h_last[2] = {0, 0};
     int voff_ah = 0;
-    if constexpr (k16) {
+    if constexpr (kB16) {
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
         const int r = 8 * wave + 4 * k + (lane >> 4);
@@ -1358,7 +1377,7 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     const int ns_loop = (ns_all + KS - 1) / KS;
     // The first RT waves also load one A tile per stage (wave 0 the one E4M3
     // tile of a stage with fp32 B; every wave a quarter of an fp32 tile).
-    const bool a_wave = wave < (kBF32 ? 1 : k16 ? kWaves : RT);
+    const bool a_wave = wave < (kBF32 ? 1 : k16 ? kWaves : kF8B16 ? 2 : RT);
     // Stages issued before the windows land (the prologue, s < kDmaStages - 1,
     // a constant after unrolling) read their columns from the work item
     // (tiles below 16); later ones from colw.
@@ -1383,13 +1402,19 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     auto issue_stage = [&](int s) {
       const int slot0 = (s % kDmaStages) * kStageTiles;
       const int base = (s * KS + sg) * kStageTiles;
-      if constexpr (k16) {
-        // One A load (half a tile) and four B loads per wave: 5 per stage.
-        {
+      if constexpr (kB16) {
+        // 16-bit tiles: one A load (half a tile) and four B loads per wave,
+        // 5 per stage.  E4M3 tiles: waves 0 and 1 load one 1 KB tile each
+        // (5 loads), the others only their four B loads.
+        if constexpr (k16) {
           const int idx = base + (wave >> 1);
           const bool live = idx < nt;
           dma_b128(da, &a_ring[slot0 + (wave >> 1)][(wave & 1) * 64], live ? voff_ah : kOutOfRange,
                    (begin + (live ? idx : 0)) * (kTile * kTile * 2));
+        } else if (a_wave) {
+          const int idx = base + wave;
+          const bool live = idx < nt;
+          dma_b128(da, &a_ring[slot0 + wave][0], live ? voff_a : kOutOfRange, (begin + (live ? idx : 0)) * (kTile * kTile));
         }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -1448,7 +1473,7 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
       // Past this group's last stage (s >= ns) ahead is negative: wait for all.
       const int ahead = min(ns - 1, s + kDmaStages - 2) - s;  // stages issued after s
       if (kF32 || k16) wait_stages<5>(ahead);
-      else if (kBF32) {
+      else if (kBF32 || kF8B16) {
         if (a_wave) wait_stages<5>(ahead);
         else wait_stages<4>(ahead);
       } else if (a_wave) wait_stages<1 + RT>(ahead);
@@ -1524,6 +1549,59 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
               acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8hf, av[h]),
                                                            __builtin_bit_cast(v8hf, bv[h]), acc, 0, 0, 0);
           }
+        }
+      } else if constexpr (kF8B16) {
+        // E4M3 tiles times a 16-bit B: lane (i, g) decodes its 16 codes of A
+        // row i (k = 16 g .. + 15) exactly to B's 16-bit type; MFMA h takes
+        // k = 16 g + 8 h .. + 7 of A and of B column 32 wave + i (two
+        // transposed reads, as for 16-bit tiles).  Each tile's product is
+        // scaled into the fp32 accumulators.
+        const int i = j & 15;
+        typedef short v4h16 __attribute__((ext_vector_type(4)));
+        typedef short v8h16 __attribute__((ext_vector_type(8)));
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const v4i araw = a_ring[slot0 + u][lane];
+          v4i a8[2];
+          {
+            uint32_t d[8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              if constexpr (ELT == kEltFp8Bf16) e4m3x4_to_bf16((uint32_t)araw[q], d[2 * q], d[2 * q + 1]);
+              else e4m3x4_to_f16((uint32_t)araw[q], d[2 * q], d[2 * q + 1]);
+            }
+            a8[0] = v4i{(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
+            a8[1] = v4i{(int)d[4], (int)d[5], (int)d[6], (int)d[7]};
+          }
+          const uint8_t* bs = &b_ring[slot0 + u][0];
+          v8h16 bv[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            v4h16 t[2];
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+              const int row = 16 * g + 8 * h + 4 * r + (i >> 2);
+              const int gq = 4 * wave + 2 * (j >> 4) + ((i & 3) >> 1);
+              const uint8_t* a = bs + row * (kPanel * 2) + ((gq ^ ((row & 3) << 2)) << 4) + 8 * (i & 1);
+              t[r] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (__attribute__((address_space(3))) v4h16*)(const_cast<uint8_t*>(a)));
+            }
+            bv[h] = v8h16{t[0][0], t[0][1], t[0][2], t[0][3], t[1][0], t[1][1], t[1][2], t[1][3]};
+          }
+          v16f part = {};
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            if constexpr (ELT == kEltFp8Bf16)
+              part = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a8[h]),
+                                                             __builtin_bit_cast(v8bf, bv[h]), part, 0, 0, 0);
+            else
+              part = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8hf, a8[h]),
+                                                            __builtin_bit_cast(v8hf, bv[h]), part, 0, 0, 0);
+          }
+          // Tiles past the item's end were loaded as zeros (a zero product).
+          const float sc = bcast(scw, min(base + u, kCgMaxTiles - 1));
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[r] = __builtin_fmaf(sc, part[r], acc[r]);
         }
       } else if constexpr (ELT == kEltFp8F32) {
         // E4M3 tile times fp32 B on the bf16 MFMA: lane (i, g) holds A row i,
@@ -2485,18 +2563,20 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
       default: return fail(VOID_ERR_UNSUPPORTED, "E4M3 x fp32 SpMM writes f32, bf16 or f16");
     }
   }
-  if (elt == kEltBf16 || elt == kEltF16) {
-    // 16-bit tiles and B: the LDS-DMA ring only (row-major B and C with
-    // 16-byte aligned rows, N % 8 == 0, items of at most 64 tiles, 31-bit
-    // byte offsets).  The Python wrapper takes the fp32 kernel otherwise.
+  if (elt == kEltBf16 || elt == kEltF16 || elt == kEltFp8Bf16 || elt == kEltFp8F16) {
+    // A 16-bit B (with 16-bit or E4M3 tiles): the LDS-DMA ring only
+    // (row-major B and C with 16-byte aligned rows, N % 8 == 0, items of at
+    // most 64 tiles, 31-bit byte offsets).  The Python wrappers take the
+    // fp32 B kernels otherwise.
     const int64_t lim = (int64_t)1 << 31;
+    const int64_t a_tile_bytes = (elt == kEltBf16 || elt == kEltF16) ? 2048 : 1024;
     const int esz = (d->out_dtype == VOID_DT_BF16 || d->out_dtype == VOID_DT_F16) ? 2 : 4;
     if (d->b_col_major || !(c_ok && (bu % 16 == 0) && (d->ldb % 8 == 0) && (d->N % 8 == 0)))
       return fail(VOID_ERR_UNSUPPORTED, "16-bit SpMM needs a row-major B, 16-byte aligned B and C rows and N %% 8 == 0");
     if (plan->chunk_tiles > kCgMaxTiles)
       return fail(VOID_ERR_ARG, "16-bit SpMM takes work items of at most %d tiles (chunk_tiles %d)", kCgMaxTiles,
                   plan->chunk_tiles);
-    if (!((int64_t)a->n_blocks * kTile * kTile * 2 < lim && (int64_t)((a->K + kTile - 1) / kTile) * kTile * d->ldb * 2 < lim &&
+    if (!((int64_t)a->n_blocks * a_tile_bytes < lim && (int64_t)((a->K + kTile - 1) / kTile) * kTile * d->ldb * 2 < lim &&
           (int64_t)a->M * d->ldc * esz < lim))
       return fail(VOID_ERR_UNSUPPORTED, "16-bit SpMM operands must stay below 2 GiB");
     // Ring shape as for int8: two rings per 8-wave workgroup for one-round
@@ -2520,8 +2600,12 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
         default: return fail(VOID_ERR_UNSUPPORTED, "16-bit SpMM writes f32, bf16 or f16");
       }
     };
-    if (elt == kEltBf16) return go16(std::integral_constant<int, kEltBf16>{});
-    return go16(std::integral_constant<int, kEltF16>{});
+    switch (elt) {
+      case kEltBf16: return go16(std::integral_constant<int, kEltBf16>{});
+      case kEltF16: return go16(std::integral_constant<int, kEltF16>{});
+      case kEltFp8Bf16: return go16(std::integral_constant<int, kEltFp8Bf16>{});
+      default: return go16(std::integral_constant<int, kEltFp8F16>{});
+    }
   }
   if (elt == kEltF32) {
     const bool vec = c_ok && (bu % 16 == 0) && (d->ldb % 4 == 0) && (d->N % 4 == 0);
@@ -2931,6 +3015,15 @@ int void_spmm_f32(const void_bsr_desc* a, const void_dense_args* d, const void_p
                   void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (d && d->out_dtype == VOID_DT_I32) return fail(VOID_ERR_UNSUPPORTED, "float SpMM writes f32, bf16 or f16");
   return run(kEltF32, a, d, VOID_EPI_PER_BLOCK, plan, workspace, workspace_bytes, stream);
+}
+
+int void_spmm_fp8_b16(const void_bsr_desc* a, const void_dense_args* d, int32_t b_dtype, const void_plan* plan,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (d && d->out_dtype == VOID_DT_I32) return fail(VOID_ERR_UNSUPPORTED, "E4M3 x 16-bit SpMM writes f32, bf16 or f16");
+  if (b_dtype != VOID_DT_BF16 && b_dtype != VOID_DT_F16)
+    return fail(VOID_ERR_ARG, "b_dtype must be VOID_DT_BF16 or VOID_DT_F16, got %d", b_dtype);
+  return run(b_dtype == VOID_DT_BF16 ? kEltFp8Bf16 : kEltFp8F16, a, d, VOID_EPI_PER_BLOCK, plan, workspace,
+             workspace_bytes, stream);
 }
 
 int void_spmm_bf16(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,

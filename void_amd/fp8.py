@@ -233,9 +233,11 @@ def void_spmm_fp8(a: FP8VOIDTensor, b: torch.Tensor, output_dtype: torch.dtype =
     """FP8 block-sparse SpMM C = A @ B (fp8.py:674-742) on the gfx950 kernels.
 
     A float B (fp32, bf16, fp16) keeps the reference's semantics: the kernel
-    computes sum_t s_t dec(A_t) @ B with B in fp32 (fp8.py:624-671 upcasts
-    both operands), here on the bf16 MFMA with A decoded exactly to bf16 and
-    B split into bf16 hi + lo (within 2^-16 relative per product).
+    computes sum_t s_t dec(A_t) @ B with B as given (fp8.py:624-671 upcasts
+    both operands).  A bf16 / fp16 B runs on the 16-bit MFMA with A decoded
+    exactly to its type (exact products); an fp32 B on the bf16 MFMA with A
+    decoded exactly and B split into bf16 hi + lo (within 2^-16 relative per
+    product).
     A float8_e4m3fn B runs on the fp8 x fp8 MFMA and is taken as the codes'
     values, as the reference's upcast does.
     b_scale (default 1.0; a scalar or N per-column scales) multiplies the
@@ -279,6 +281,21 @@ def void_spmm_fp8(a: FP8VOIDTensor, b: torch.Tensor, output_dtype: torch.dtype =
                                bias=bias, chunk=chunk)
     if chunk > tuning.FP32_B_MAX_CHUNK:
         raise ValueError(f"a float B takes chunk_tiles <= {tuning.FP32_B_MAX_CHUNK}, got {chunk}")
+    if b.dtype in (torch.bfloat16, torch.float16):
+        # A 16-bit B is taken as it is, on the 16-bit MFMA (A decoded exactly
+        # to its type), when its rows and the output's are 16-byte aligned
+        # and N % 8 == 0; otherwise it is widened to fp32 below.
+        b16 = b if b.stride(1) == 1 else b.contiguous()
+        if (N % 8 == 0 and b16.stride(0) % 8 == 0 and b16.data_ptr() % 16 == 0 and a.n_blocks * 1024 < (1 << 31)
+                and (K + 31) // 32 * 32 * b16.stride(0) * 2 < (1 << 31) and M * N * out.element_size() < (1 << 31)):
+            kind = "fp8_bf16b" if b.dtype == torch.bfloat16 else "fp8_f16b"
+            aligned = out.stride(1) == 1 and out.data_ptr() % 16 == 0 and out.stride(0) % 4 == 0
+            tgt = out if aligned else torch.empty(M, N, dtype=output_dtype, device=b.device)
+            _runtime.launch(kind, a.device_bsr(), b16, b_scale=scalar_scale, b_scale_vec=scale_vec,
+                            out=tgt, epilogue=_lib.EPI_PER_BLOCK, activation=act, bias=bias, chunk=chunk)
+            if tgt is not out:
+                out.copy_(tgt)
+            return out
     # fp32 B, row-major with 16-byte aligned rows and N % 4 == 0 (the ring
     # kernel's layout); other widths run on zero-padded columns.
     N4 = (N + 3) // 4 * 4
