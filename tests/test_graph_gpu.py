@@ -126,3 +126,11 @@ def test_graph_bf16(gpu):
     plan = vt.device_bsr(torch.bfloat16).plan(12)
     assert plan.n_split_tiles > 0
     _capture_and_check(lambda: float_spmm(vt, b, plan=plan), _other(gpu))
+
+
+def test_graph_fp8_bf16_b(gpu):
+    """E4M3 tiles times a bf16 B (void_spmm_fp8_b16), fp16 output."""
+    case = cases.uniform_blocks(512, 1024, 256, 250, seed=16)
+    f8 = void_amd.void_tensor_to_fp8(cases.make_void_tensor(case, "cpu")).to(gpu)
+    bt = torch.from_numpy(case.b).to(torch.bfloat16).to(gpu)
+    _capture_and_check(lambda: void_amd.void_spmm_fp8(f8, bt, output_dtype=torch.float16), _other(gpu))
