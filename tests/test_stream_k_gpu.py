@@ -112,3 +112,32 @@ def test_stream_k_bf16_and_empty_rows(gpu):
     for r in rows_empty:
         assert not np.any(got[r * 32:(r + 1) * 32])
     assert np.allclose(got, ref, rtol=2.0 ** -8, atol=1e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_stream_k_16bit_tensor(gpu, dtype):
+    """A 16-bit VOID tensor with a B of its dtype runs the workload on the
+    16-bit kernel (no fp32 copy of the tiles is made); split rows are
+    reduced deterministically."""
+    rng = np.random.default_rng(9)
+    nbr = 64
+    counts = np.minimum(rng.zipf(1.5, nbr), 200)
+    br = np.repeat(np.arange(nbr), counts)
+    bc = np.concatenate([rng.choice(256, c, replace=False) for c in counts])
+    tiles = rng.standard_normal((len(br), 32, 32)).astype(np.float32)
+    case = cases.BlockCase("zipf16", nbr * 32, 256 * 32, 128, *cases._sorted(tiles, br, bc),
+                           rng.standard_normal((256 * 32, 128)).astype(np.float32))
+    vt = cases.make_void_tensor(case, "cpu").to_dtype(dtype).to(gpu)
+    w = compute_stream_k_workload(vt, max_work_per_worker=16)
+    B = torch.from_numpy(case.b).to(dtype).to(gpu)
+    out = void_spmm_stream_k(vt, B, workload=w)
+    assert out.dtype == dtype
+    assert set(vt._device_bsr) == {f"{B.device}/{dtype}"}
+    again = void_spmm_stream_k(vt, B, workload=w)
+    assert torch.equal(out, again)
+    A = _dense_of(vt)
+    Bd = B.double().cpu().numpy()
+    ref = A @ Bd
+    n = 32 * int(counts.max())
+    tol = n * 2.0 ** -24 * (np.abs(A) @ np.abs(Bd)) + (2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11) * np.abs(ref) + 2.0 ** -24
+    assert np.all(np.abs(out.double().cpu().numpy() - ref) <= tol)

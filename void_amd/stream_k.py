@@ -92,7 +92,11 @@ def workload_plan(void_tensor, workload: StreamKWorkload) -> "_runtime.DevicePla
     """Device work items that run exactly the workload's worker ranges,
     cached on the tensor's device view per workload object."""
     from .ops import F32_CHUNK
-    dbsr = void_tensor.device_bsr()
+    # Plans depend only on the block structure, which every device copy of
+    # the tiles shares: take the copy in the tiles' own dtype (the one the
+    # 16-bit kernel uses for 16-bit tensors) rather than make another.
+    dt = void_tensor.values.dtype
+    dbsr = void_tensor.device_bsr(dt if dt in (torch.bfloat16, torch.float16) else torch.float32)
     key = ("workload", id(workload))
     cached = dbsr.plans.get(key)
     if cached is not None and cached[0] is workload:
@@ -113,7 +117,8 @@ def workload_plan(void_tensor, workload: StreamKWorkload) -> "_runtime.DevicePla
 def void_spmm_stream_k(a, b: torch.Tensor, workload: Optional[StreamKWorkload] = None,
                        out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Stream-K load-balanced SpMM C = A @ B for a float VOIDTensor
-    (stream_k.py:233-301), on the fp32 MFMA kernel of libvoid_amd.so.
+    (stream_k.py:233-301), on the float MFMA kernels of libvoid_amd.so (the
+    16-bit one when the tiles and B share a 16-bit dtype).
 
     Each worker of ``workload`` (computed by compute_stream_k_workload when
     None) becomes one work item over its tile range; the partial blocks of a
