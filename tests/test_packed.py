@@ -33,11 +33,13 @@ def test_header_layout_known_answer():
     assert np.array_equal(tiles, vt.values.numpy()[order])
 
 
-@pytest.mark.parametrize("kind", ["float", "int8", "int8_tensor", "fp8"])
+@pytest.mark.parametrize("kind", ["float", "bf16", "f16", "int8", "int8_tensor", "fp8"])
 def test_round_trip_cpu(kind):
     vt = _vt(seed=3)
     if kind == "float":
         t = vt
+    elif kind in ("bf16", "f16"):
+        t = vt.to_dtype(torch.bfloat16 if kind == "bf16" else torch.float16)
     elif kind == "int8":
         t = void_amd.quantize_void_tensor(vt)
     elif kind == "int8_tensor":
@@ -51,7 +53,8 @@ def test_round_trip_cpu(kind):
         assert torch.equal(u.values_fp8.view(torch.uint8), t.values_fp8.view(torch.uint8))
         assert torch.equal(u.scaling_info.scale, t.scaling_info.scale)
         assert torch.equal(u.morton_codes, t.morton_codes)
-    elif kind == "float":
+    elif kind in ("float", "bf16", "f16"):
+        assert u.values.dtype == t.values.dtype and u.dtype == t.values.dtype
         assert torch.equal(u.values, t.values) and torch.equal(u.morton_codes, t.morton_codes)
     else:
         assert torch.equal(u.values, t.values) and torch.equal(u.scales, t.scales)
@@ -124,3 +127,33 @@ def test_fused_sparse_linear(gpu, act):
                                    + np.abs(layer.bias.detach().cpu().double().numpy())[None, :])
     err = np.abs(y.reshape(-1, 256).detach().cpu().double().numpy() - ref)
     assert np.all(err <= bound + 8 * 2.0 ** -24 * np.abs(ref) + 1e-6)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gpu_load_16bit_feeds_kernel(gpu, dtype):
+    """A 16-bit blob loads as a 16-bit tensor whose prebuilt device copy the
+    16-bit SpMM uses directly, with the same bits as the tensor it came
+    from; FusedSparseLinear over it runs in that dtype."""
+    case = cases.uniform_blocks(256, 512, 64, 60, seed=4)
+    vt = cases.make_void_tensor(case, "cpu").to_dtype(dtype)
+    u = packed.unpack(packed.pack(vt), gpu)
+    assert u.values.dtype == dtype and set(u._device_bsr) == {f"{gpu}/{dtype}"}
+    b = torch.from_numpy(case.b).to(dtype).to(gpu)
+    got = void_amd.void_spmm(u, b)
+    ref = void_amd.void_spmm(vt.to(gpu), b)
+    assert torch.equal(got, ref)
+    layer = void_amd.FusedSparseLinear.from_packed(packed.pack(vt), device=gpu, activation="relu").to(dtype)
+    x = torch.randn(5, 512, device=gpu).to(dtype)
+    y = layer(x)
+    assert y.dtype == dtype
+    W = vt.values.float()
+    Wd = oracle.densify(W.numpy(), case.block_rows, case.block_cols, (256, 512)).astype(np.float64)
+    X = x.double().cpu().numpy()
+    pre = X @ Wd.T + layer.bias.detach().double().cpu().numpy()[None, :]
+    ref = np.maximum(pre, 0)
+    n = 32 * np.bincount(case.block_rows).max() + 1
+    rel = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    bound = n * 2.0 ** -24 * (np.abs(X) @ np.abs(Wd).T + np.abs(layer.bias.detach().double().cpu().numpy())) \
+        + rel * np.abs(ref) + 2.0 ** -24
+    assert np.all(np.abs(y.double().cpu().numpy() - ref) <= bound)

@@ -10,7 +10,8 @@ Layout (offsets in bytes; sections 256-byte aligned):
 
     0   magic  b"VOIDBSR\\0"
     8   u32    version (1)
-    12  u32    kind: 0 float32 tiles, 1 int8 tiles, 2 float8_e4m3fn tiles
+    12  u32    kind: 0 float32 tiles, 1 int8 tiles, 2 float8_e4m3fn tiles,
+               3 bfloat16 tiles, 4 float16 tiles
     16  i64    M          24 i64 K
     32  i64    n_blocks   40 i64 n_block_rows
     48  u32    tile (32)  52 u32 flags (bit 0: one per-tensor scale)
@@ -36,7 +37,9 @@ from .format import VOIDTensor, build_bsr_layout, morton_encode_batch
 
 MAGIC = b"VOIDBSR\0"
 VERSION = 1
-KIND_F32, KIND_I8, KIND_FP8 = 0, 1, 2
+KIND_F32, KIND_I8, KIND_FP8, KIND_BF16, KIND_F16 = 0, 1, 2, 3, 4
+_FLOAT_KINDS = {KIND_F32: torch.float32, KIND_BF16: torch.bfloat16, KIND_F16: torch.float16}
+_ELT_BYTES = {KIND_F32: 4, KIND_I8: 1, KIND_FP8: 1, KIND_BF16: 2, KIND_F16: 2}
 _HEADER = struct.Struct("<8sIIqqqqIIQQQQQq")
 _ALIGN = 256
 
@@ -59,6 +62,12 @@ def _parts(t):
             raise NotImplementedError("packed blobs hold per-block E4M3 tiles")
         return KIND_FP8, t.values_fp8.view(torch.uint8), t.scaling_info.scale, False
     if isinstance(t, VOIDTensor):
+        # 16-bit tiles keep their dtype (and feed the 16-bit kernel when
+        # loaded); other float dtypes are stored as fp32.
+        if t.values.dtype == torch.bfloat16:
+            return KIND_BF16, t.values.view(torch.int16), None, False
+        if t.values.dtype == torch.float16:
+            return KIND_F16, t.values.view(torch.int16), None, False
         return KIND_F32, t.values.to(torch.float32), None, False
     raise TypeError(f"cannot pack {type(t).__name__}")
 
@@ -73,7 +82,7 @@ def pack(t) -> bytes:
     lay = build_bsr_layout(t.block_rows, t.block_cols, n_br, n_bc, torch.device("cpu"))
     order = lay.order.numpy()
     tiles_np = tiles.detach().cpu().contiguous().numpy()[order] if t.n_blocks else tiles.detach().cpu().numpy()
-    if kind == KIND_F32:
+    if kind in _FLOAT_KINDS:
         sc = np.zeros(0, np.float32)
     else:
         s = scales.detach().cpu().to(torch.float32).numpy().reshape(-1)
@@ -107,11 +116,11 @@ def unpack(blob: Union[bytes, bytearray, memoryview], device: Union[str, torch.d
         _HEADER.unpack_from(mv, 0)
     if magic != MAGIC or version != VERSION:
         raise ValueError("not a VOID packed BSR blob (version 1)")
-    if tile != 32 or n_br != (M + 31) // 32 or total > len(mv) or kind not in (KIND_F32, KIND_I8, KIND_FP8):
+    if tile != 32 or n_br != (M + 31) // 32 or total > len(mv) or kind not in _ELT_BYTES:
         raise ValueError("corrupt VOID packed BSR blob header")
     per_tensor = bool(flags & 1)
-    elt = 4 if kind == KIND_F32 else 1
-    n_sc = 0 if kind == KIND_F32 else (1 if per_tensor else nb)
+    elt = _ELT_BYTES[kind]
+    n_sc = 0 if kind in _FLOAT_KINDS else (1 if per_tensor else nb)
     for o, n in ((o_rp, 4 * (n_br + 1)), (o_ci, 4 * nb), (o_sc, 4 * n_sc), (o_ti, elt * 1024 * nb)):
         if o % _ALIGN or o + n > total:
             raise ValueError("corrupt VOID packed BSR blob sections")
@@ -147,12 +156,14 @@ def unpack(blob: Union[bytes, bytearray, memoryview], device: Union[str, torch.d
                               row_ptr_host=rp_host, col_idx_host=ci_host, per_tensor=per_tensor or n_sc == 0,
                               M=M, K=K, n_blocks=nb, n_block_rows=n_br, order=order)
     key = str(dev)
-    if kind == KIND_F32:
-        vals = tiles_bytes.view(torch.float32).view(nb, 32, 32).index_select(0, perm_t)
+    if kind in _FLOAT_KINDS:
+        dt = _FLOAT_KINDS[kind]
+        vals = tiles_bytes.view(dt).view(nb, 32, 32).index_select(0, perm_t)
         vt = VOIDTensor(values=vals, block_rows=block_rows, block_cols=block_cols, morton_codes=morton_t,
-                        shape=(M, K), tile_size=(32, 32), nnz_original=nnz, n_blocks=nb, density=density)
+                        shape=(M, K), tile_size=(32, 32), nnz_original=nnz, n_blocks=nb, density=density, dtype=dt)
         dbsr.src_key = _runtime.source_key(vals)
-        vt._device_bsr[key] = dbsr
+        # The device copy under the key the float SpMM looks up for this dtype.
+        vt._device_bsr[key if dt == torch.float32 else f"{dev}/{dt}"] = dbsr
         return vt
     if kind == KIND_I8:
         from .int_quant import Int8VOIDTensor, IntQuantConfig, ScaleMode
