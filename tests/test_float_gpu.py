@@ -19,15 +19,16 @@ pytestmark = pytest.mark.gpu
 U = 2.0 ** -24
 
 
-@pytest.fixture(params=["ring", "f32"])
+@pytest.fixture(params=["ring", "cgd", "cgdk", "f32"])
 def fkernel(request, monkeypatch):
-    """The float tiles' two kernels: the column-group LDS-DMA ring (default
-    for row-major 16-byte aligned B; elsewhere the fallback runs anyway) and
-    the fp32 kernel of its own (VOID_AMD_KERNEL=f32)."""
-    if request.param == "f32":
-        monkeypatch.setenv("VOID_AMD_KERNEL", "f32")
-    else:
+    """The float tiles' kernels: the column-group LDS-DMA ring (default for
+    row-major 16-byte aligned B, elsewhere the fallback runs anyway) with its
+    default ring shape, forced to one ring per workgroup (cgd) or two
+    (cgdk), and the fp32 kernel of its own (VOID_AMD_KERNEL=f32)."""
+    if request.param == "ring":
         monkeypatch.delenv("VOID_AMD_KERNEL", raising=False)
+    else:
+        monkeypatch.setenv("VOID_AMD_KERNEL", request.param)
     return request.param
 
 

@@ -46,8 +46,19 @@ def _check(got, ref, bound, out_dtype):
 _C3 = {}
 
 
+@pytest.fixture(params=["default", "cgd", "cgdk"])
+def ring(request, monkeypatch):
+    """Ring shapes of the E4M3 x float-B kernels: the default, one ring per
+    workgroup, two rings per 8-wave workgroup."""
+    if request.param == "default":
+        monkeypatch.delenv("VOID_AMD_KERNEL", raising=False)
+    else:
+        monkeypatch.setenv("VOID_AMD_KERNEL", request.param)
+    return request.param
+
+
 @pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32], ids=["f16", "bf16", "f32"])
-def test_c3_fp8_float_b_full(gpu, out_dtype):
+def test_c3_fp8_float_b_full(gpu, ring, out_dtype):
     """Config 3's A (4096^2, 80 % block sparsity, E4M3 per-tile) times its
     B kept in fp32, the reference's default call (float B, fp16 output)."""
     if not _C3:
@@ -68,7 +79,7 @@ def test_c3_fp8_float_b_full(gpu, out_dtype):
 
 
 @pytest.mark.parametrize("M,K,N", [(333, 555, 64), (100, 70, 37), (64, 200, 130), (32, 32, 1), (1000, 96, 257)])
-def test_fp8_float_b_ragged(gpu, M, K, N):
+def test_fp8_float_b_ragged(gpu, ring, M, K, N):
     """Ragged M and K (edge tiles, a last B slab crossing K) and N not a
     multiple of 4 (the wrapper pads B's columns)."""
     rng = np.random.default_rng(M + K + N)
@@ -80,7 +91,7 @@ def test_fp8_float_b_ragged(gpu, M, K, N):
 
 
 @pytest.mark.parametrize("chunk", [1, 3, 7])
-def test_fp8_float_b_split_rows(gpu, chunk):
+def test_fp8_float_b_split_rows(gpu, ring, chunk):
     """Forced Stream-K splits: partial blocks reduced in chunk order."""
     case = cases.uniform_blocks(1024, 2048, 256, 900, seed=3)
     f8, A, Aabs = _setup(case)
@@ -133,15 +144,6 @@ def test_fp8_float_b_differs_from_quantised_b(gpu):
 # A 16-bit B (void_spmm_fp8_b16): the E4M3 codes decoded exactly to B's type
 # on the 16-bit MFMA, exact products; the same bar as the fp32 B.
 _B16 = [torch.bfloat16, torch.float16]
-
-
-@pytest.fixture(params=["default", "cgd", "cgdk"])
-def ring(request, monkeypatch):
-    if request.param == "default":
-        monkeypatch.delenv("VOID_AMD_KERNEL", raising=False)
-    else:
-        monkeypatch.setenv("VOID_AMD_KERNEL", request.param)
-    return request.param
 
 
 def _b16_ref(A, Aabs, b16, sb=1.0):

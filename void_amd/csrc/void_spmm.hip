@@ -1133,8 +1133,7 @@ template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false, int RT = kDmaT
 __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     DMA ? (KS > 1 ? 4 : dma_waves_per_eu(RT)) : 2, DMA ? (KS > 1 ? 4 : dma_waves_per_eu(RT)) : 2))) void spmm_cg_kernel(Params p) {
   static_assert(!(DMA && BCOL), "the LDS-DMA ring is for row-major B");
-  static_assert(KS == 1 || (DMA && ELT != kEltF32 && ELT != kEltFp8F32 && KS == 2),
-                "the two-ring split is for int8 / fp8 / 16-bit B on the LDS-DMA ring");
+  static_assert(KS == 1 || (DMA && KS == 2), "the two-ring split is for the LDS-DMA ring");
   using A = Accum1<ELT, EPI>;
   constexpr bool kInt = A::kInt;
   constexpr bool kF32 = ELT == kEltF32;                     // fp32 A tiles
@@ -2423,6 +2422,15 @@ int n_panels_for(int32_t N) { return (N + kPanel - 1) / kPanel; }
 
 unsigned long long* g_trace = nullptr;  // set by void_debug_set_trace in instrumented builds
 
+// Ring shape of the 16-bit and fp32-B kernels, as for int8: two rings per
+// 8-wave workgroup for one-round grids and split plans below four rounds,
+// one ring otherwise.  VOID_AMD_KERNEL=cgdk / cgd force one or the other.
+bool two_rings(int32_t n_split_tiles, int64_t grid) {
+  const char* fk = getenv("VOID_AMD_KERNEL");
+  if (fk && (strcmp(fk, "cgdk") == 0 || strcmp(fk, "cgd") == 0)) return strcmp(fk, "cgdk") == 0;
+  return n_split_tiles > 0 ? grid < kDeepGridRounds * 1024 : grid <= kPairGridMax;
+}
+
 // Split-row counters and partials at fixed places (the allocation-free entry
 // point's scratch) in place of a caller's workspace.
 struct FixedScratch {
@@ -2556,10 +2564,17 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
     if (!((int64_t)a->n_blocks * kTile * kTile < lim && (int64_t)((a->K + kTile - 1) / kTile) * kTile * d->ldb * 4 < lim &&
           (int64_t)a->M * d->ldc * esz < lim))
       return fail(VOID_ERR_UNSUPPORTED, "E4M3 x fp32 SpMM operands must stay below 2 GiB");
+    const bool pair = two_rings(n_split_tiles, grid);
     switch (d->out_dtype) {
-      case VOID_DT_F32: return launch_cg<kEltFp8F32, VOID_EPI_PER_BLOCK, VOID_DT_F32, false, true>(p, grid, stream);
-      case VOID_DT_BF16: return launch_cg<kEltFp8F32, VOID_EPI_PER_BLOCK, VOID_DT_BF16, false, true>(p, grid, stream);
-      case VOID_DT_F16: return launch_cg<kEltFp8F32, VOID_EPI_PER_BLOCK, VOID_DT_F16, false, true>(p, grid, stream);
+      case VOID_DT_F32:
+        return pair ? launch_cg<kEltFp8F32, VOID_EPI_PER_BLOCK, VOID_DT_F32, false, true, kDmaTiles, 2>(p, grid, stream)
+                    : launch_cg<kEltFp8F32, VOID_EPI_PER_BLOCK, VOID_DT_F32, false, true>(p, grid, stream);
+      case VOID_DT_BF16:
+        return pair ? launch_cg<kEltFp8F32, VOID_EPI_PER_BLOCK, VOID_DT_BF16, false, true, kDmaTiles, 2>(p, grid, stream)
+                    : launch_cg<kEltFp8F32, VOID_EPI_PER_BLOCK, VOID_DT_BF16, false, true>(p, grid, stream);
+      case VOID_DT_F16:
+        return pair ? launch_cg<kEltFp8F32, VOID_EPI_PER_BLOCK, VOID_DT_F16, false, true, kDmaTiles, 2>(p, grid, stream)
+                    : launch_cg<kEltFp8F32, VOID_EPI_PER_BLOCK, VOID_DT_F16, false, true>(p, grid, stream);
       default: return fail(VOID_ERR_UNSUPPORTED, "E4M3 x fp32 SpMM writes f32, bf16 or f16");
     }
   }
@@ -2579,13 +2594,7 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
     if (!((int64_t)a->n_blocks * a_tile_bytes < lim && (int64_t)((a->K + kTile - 1) / kTile) * kTile * d->ldb * 2 < lim &&
           (int64_t)a->M * d->ldc * esz < lim))
       return fail(VOID_ERR_UNSUPPORTED, "16-bit SpMM operands must stay below 2 GiB");
-    // Ring shape as for int8: two rings per 8-wave workgroup for one-round
-    // grids and split plans below four rounds, one ring otherwise
-    // (VOID_AMD_KERNEL=cgdk / cgd force one or the other).
-    const char* fk = getenv("VOID_AMD_KERNEL");
-    const bool pair = fk && (strcmp(fk, "cgdk") == 0 || strcmp(fk, "cgd") == 0)
-                          ? strcmp(fk, "cgdk") == 0
-                          : (n_split_tiles > 0 ? grid < kDeepGridRounds * 1024 : grid <= kPairGridMax);
+    const bool pair = two_rings(n_split_tiles, grid);
     auto go16 = [&](auto elt_c) -> int {
       constexpr int E = decltype(elt_c)::value;
       auto pick = [&](auto out_c) -> int {
@@ -2619,10 +2628,17 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
                          (int64_t)((a->K + kTile - 1) / kTile) * kTile * d->ldb * 4 < lim &&
                          (int64_t)a->M * d->ldc * 4 < lim && !(fk && strcmp(fk, "f32") == 0);
     if (ring_ok) {
+      const bool pair = two_rings(n_split_tiles, grid);
       switch (d->out_dtype) {
-        case VOID_DT_F32: return launch_cg<kEltF32, VOID_EPI_PER_BLOCK, VOID_DT_F32, false, true>(p, grid, stream);
-        case VOID_DT_BF16: return launch_cg<kEltF32, VOID_EPI_PER_BLOCK, VOID_DT_BF16, false, true>(p, grid, stream);
-        case VOID_DT_F16: return launch_cg<kEltF32, VOID_EPI_PER_BLOCK, VOID_DT_F16, false, true>(p, grid, stream);
+        case VOID_DT_F32:
+          return pair ? launch_cg<kEltF32, VOID_EPI_PER_BLOCK, VOID_DT_F32, false, true, kDmaTiles, 2>(p, grid, stream)
+                      : launch_cg<kEltF32, VOID_EPI_PER_BLOCK, VOID_DT_F32, false, true>(p, grid, stream);
+        case VOID_DT_BF16:
+          return pair ? launch_cg<kEltF32, VOID_EPI_PER_BLOCK, VOID_DT_BF16, false, true, kDmaTiles, 2>(p, grid, stream)
+                      : launch_cg<kEltF32, VOID_EPI_PER_BLOCK, VOID_DT_BF16, false, true>(p, grid, stream);
+        case VOID_DT_F16:
+          return pair ? launch_cg<kEltF32, VOID_EPI_PER_BLOCK, VOID_DT_F16, false, true, kDmaTiles, 2>(p, grid, stream)
+                      : launch_cg<kEltF32, VOID_EPI_PER_BLOCK, VOID_DT_F16, false, true>(p, grid, stream);
         default: return fail(VOID_ERR_UNSUPPORTED, "float SpMM writes f32, bf16 or f16");
       }
     }
