@@ -292,6 +292,15 @@ int void_spmm_bf16(const void_bsr_desc* a, const void_dense_args* d, const void_
 int void_spmm_f16(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
                   void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* dst[c * ld_dst + r] = src[r * ld_src + c] for a rows x cols byte matrix:
+ * a column-major int8 or E4M3 B (src: its N columns of K bytes, ld_src
+ * between columns; rows = N, cols = K) made row-major (dst: K x N,
+ * ld_dst >= N) for the LDS-DMA ring, which reads B slabs in whole lines.
+ * rows, cols, ld_src and ld_dst multiples of 16, 16-byte aligned arrays.  No
+ * counterpart in the reference (its kernels take B's strides as given). */
+int void_transpose_b8(const void* src, int64_t ld_src, int32_t rows, int32_t cols, void* dst, int64_t ld_dst,
+                      hipStream_t stream);
+
 /* ---- Quantisers on the path's input side (one wave per tile) ---------- */
 
 /* Per-tile symmetric INT8 of n_tiles fp32 32x32 tiles (tile t at

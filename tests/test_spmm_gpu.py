@@ -302,6 +302,23 @@ def test_column_major_b(gpu, kernel):
     assert np.array_equal(raw.cpu().numpy(), oracle.i8_acc(A, bq))
 
 
+@pytest.mark.parametrize("copy", ["0", "1"])
+def test_column_major_b_copy(gpu, copy, monkeypatch):
+    """A column-major B is used in place (VOID_AMD_BT=0) or copied to row-major
+    for the LDS-DMA ring (1; the default on dense enough grids): the same
+    int32 accumulators and row-mean bits either way."""
+    monkeypatch.setenv("VOID_AMD_BT", copy)
+    case = cases.uniform_blocks(640, 1024, 384, 600, seed=19)
+    qd, A, bq, bs = _int8_setup(case, gpu)
+    bt_cm = torch.from_numpy(np.ascontiguousarray(bq.T)).to(gpu).t()
+    st = torch.from_numpy(bs).to(gpu)
+    acc = oracle.i8_acc(A, bq)
+    raw = void_amd.void_spmm_int8(qd, bt_cm, b_scale=st, epilogue="raw_i32")
+    rm = void_amd.void_spmm_int8(qd, bt_cm, b_scale=st, epilogue="row_mean")
+    assert np.array_equal(raw.cpu().numpy(), acc)
+    assert np.array_equal(rm.cpu().numpy().view(np.int32), oracle.row_mean(A, acc, bs).view(np.int32))
+
+
 def test_gelu_bf16_bias(gpu, kernel):
     case = cases.uniform_blocks(256, 512, 192, 60, seed=11)
     qd, A, bq, bs = _int8_setup(case, gpu)
@@ -422,3 +439,18 @@ def test_inplace_updates_are_seen(gpu):
     z1 = void_amd.void_spmm_fp8(f8, b8, output_dtype=torch.float32, b_scale=float(b8s))
     f8.scaling_info.scale.mul_(2.0)
     assert torch.equal(void_amd.void_spmm_fp8(f8, b8, output_dtype=torch.float32, b_scale=float(b8s)), 2.0 * z1)
+
+
+@pytest.mark.parametrize("rows,cols,pad", [(16, 16, 0), (384, 1024, 0), (2048, 4096, 0), (48, 272, 32), (1040, 80, 16)])
+def test_transpose_b8(gpu, rows, cols, pad):
+    """void_transpose_b8 (a column-major 8-bit B made row-major): every byte
+    lands at its transposed place, tile edges and padded rows included."""
+    from void_amd import _lib
+    g = torch.Generator().manual_seed(rows + cols)
+    src = torch.randint(-128, 128, (rows, cols + pad), dtype=torch.int8, generator=g).to(gpu)
+    dst = torch.full((cols, rows + 16), 7, dtype=torch.int8, device=gpu)
+    st = _lib.lib().void_transpose_b8(src.data_ptr(), cols + pad, rows, cols, dst.data_ptr(), rows + 16,
+                                      torch.cuda.current_stream(gpu).cuda_stream)
+    _lib.check(st, "void_transpose_b8")
+    assert torch.equal(dst[:, :rows], src[:, :cols].t())
+    assert torch.all(dst[:, rows:] == 7)

@@ -351,6 +351,21 @@ def dense_operand(b: torch.Tensor) -> Tuple[torch.Tensor, int, bool]:
     return b, b.shape[1], False
 
 
+def row_major_copy_b8(b: torch.Tensor, ld: int) -> torch.Tensor:
+    """Row-major K x N copy of a column-major 8-bit B (N columns of K bytes,
+    ld apart): void_transpose_b8 where the shape allows, torch's copy
+    otherwise."""
+    K, N = b.shape
+    out = torch.empty(K, N, dtype=b.dtype, device=b.device)
+    if K % 16 == 0 and N % 16 == 0 and ld % 16 == 0 and b.data_ptr() % 16 == 0:
+        st = _lib.lib().void_transpose_b8(b.data_ptr(), ld, N, K, out.data_ptr(), N,
+                                          torch.cuda.current_stream(b.device).cuda_stream)
+        _lib.check(st, "void_transpose_b8")
+        return out
+    out.copy_(b)
+    return out
+
+
 def launch(kind: str, dbsr: DeviceBsr, b: torch.Tensor, *, b_scale: float = 1.0,
            b_scale_vec: Optional[torch.Tensor] = None, out: torch.Tensor, epilogue: int,
            activation: int = _lib.ACT_NONE, bias: Optional[torch.Tensor] = None,
@@ -359,6 +374,8 @@ def launch(kind: str, dbsr: DeviceBsr, b: torch.Tensor, *, b_scale: float = 1.0,
     lib = _lib.lib()
     N = b.shape[1]
     b_t, ldb, col_major = dense_operand(b)
+    if col_major and kind in ("int8", "fp8") and tuning.copy_col_major_b(dbsr.n_blocks, dbsr.K):
+        b_t, ldb, col_major = row_major_copy_b8(b_t, ldb), N, False  # for the LDS-DMA ring
     target = out
     if out.stride(1) != 1 or out.stride(0) < N:
         target = torch.empty(out.shape, dtype=out.dtype, device=out.device)

@@ -143,9 +143,67 @@ int check_args(const float* tiles, int32_t n_tiles, const void* q, const float* 
   return 1;
 }
 
+// dst[c][r] = src[r][c] for a rows x cols byte matrix (int8 or E4M3 codes):
+// a column-major B made row-major for the SpMM's LDS-DMA ring.  A workgroup
+// moves a 64-row x 256-column tile through LDS: 16-byte loads along the
+// source rows, then 16-byte stores along the destination rows, each built
+// from 16 bytes of one LDS column.  rows and cols are multiples of 16.
+constexpr int kTRows = 64, kTCols = 256, kTPad = 16;
+
+__global__ __launch_bounds__(256) void transpose_b8_kernel(const uint8_t* __restrict__ src, int64_t ld_src,
+                                                          int32_t rows, int32_t cols, uint8_t* __restrict__ dst,
+                                                          int64_t ld_dst) {
+  __shared__ __attribute__((aligned(16))) uint8_t t[kTRows][kTCols + kTPad];
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  const int r0 = blockIdx.y * kTRows, c0 = blockIdx.x * kTCols;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = tid + 256 * i, r = q >> 4, ch = q & 15;
+    v4i v = v4i{0, 0, 0, 0};
+    if (r0 + r < rows && c0 + 16 * ch < cols)
+      v = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(src + (int64_t)(r0 + r) * ld_src + c0 + 16 * ch));
+    *reinterpret_cast<v4i*>(&t[r][16 * ch]) = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = tid + 256 * i, c = q >> 2, rc = q & 3;
+    if (c0 + c < cols && r0 + 16 * rc < rows) {
+      uint32_t w[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        w[k] = (uint32_t)t[16 * rc + 4 * k][c] | ((uint32_t)t[16 * rc + 4 * k + 1][c] << 8) |
+               ((uint32_t)t[16 * rc + 4 * k + 2][c] << 16) | ((uint32_t)t[16 * rc + 4 * k + 3][c] << 24);
+      *reinterpret_cast<v4i*>(dst + (int64_t)(c0 + c) * ld_dst + r0 + 16 * rc) =
+          v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
+
+int void_transpose_b8(const void* src, int64_t ld_src, int32_t rows, int32_t cols, void* dst, int64_t ld_dst,
+                      hipStream_t stream) {
+  void_internal_fail(VOID_OK, "");
+  if (rows < 0 || cols < 0) return void_internal_fail(VOID_ERR_ARG, "negative size");
+  if ((int64_t)rows * cols == 0) return VOID_OK;
+  if (!src || !dst) return void_internal_fail(VOID_ERR_ARG, "null pointer");
+  if (rows % 16 || cols % 16 || ld_src < cols || ld_dst < rows || ld_src % 16 || ld_dst % 16 ||
+      ((uintptr_t)src | (uintptr_t)dst) % 16)
+    return void_internal_fail(VOID_ERR_UNSUPPORTED,
+                              "void_transpose_b8 needs rows, cols and leading dimensions multiples of 16 and "
+                              "16-byte aligned arrays");
+  const dim3 grid((cols + kTCols - 1) / kTCols, (rows + kTRows - 1) / kTRows);
+  if (grid.y > 65535) return void_internal_fail(VOID_ERR_ARG, "too many rows");
+  hipLaunchKernelGGL(transpose_b8_kernel, grid, dim3(256), 0, stream, static_cast<const uint8_t*>(src), ld_src, rows,
+                     cols, static_cast<uint8_t*>(dst), ld_dst);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return void_internal_fail(VOID_ERR_HIP, hipGetErrorString(e));
+  return VOID_OK;
+}
 
 int void_quantize_tiles_i8(const float* tiles, int32_t n_tiles, int8_t* q, float* scales, hipStream_t stream) {
   void_internal_fail(VOID_OK, "");

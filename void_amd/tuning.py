@@ -89,3 +89,21 @@ def use_row_groups(n_blocks: int, n_steps: int, n_groups: int, N: int, max_stage
     if n_steps <= 0 or max_stages > ROW_GROUP_MAX_STAGES:
         return False
     return n_groups * n_panels(max(N, 1)) >= ROW_GROUP_MIN_WORKGROUPS and n_blocks / n_steps >= min_sharing
+
+
+# A column-major B (X.t() of token-major activations) runs the register-staged
+# column-group loop, whose 16-byte loads from one column each use a quarter
+# of a 128-byte line; the LDS-DMA ring reads row-major B in whole lines.  When
+# the slabs gathered (32 N bytes per tile) exceed 32 times B itself, a
+# row-major copy of B (one pass over it) pays for itself: on the FFN config
+# the SpMM with GELU took 183 us with B column-major against 91 us
+# row-major.  VOID_AMD_BT=0 / 1 forces the copy off / on.
+COL_MAJOR_COPY_RATIO = 32
+
+
+def copy_col_major_b(n_blocks: int, K: int) -> bool:
+    import os
+    env = os.environ.get("VOID_AMD_BT")
+    if env in ("0", "1"):
+        return env == "1"
+    return 32 * n_blocks >= COL_MAJOR_COPY_RATIO * max(K, 1)
