@@ -134,3 +134,13 @@ def test_graph_fp8_bf16_b(gpu):
     f8 = void_amd.void_tensor_to_fp8(cases.make_void_tensor(case, "cpu")).to(gpu)
     bt = torch.from_numpy(case.b).to(torch.bfloat16).to(gpu)
     _capture_and_check(lambda: void_amd.void_spmm_fp8(f8, bt, output_dtype=torch.float16), _other(gpu))
+
+
+def test_graph_int8_float_b(gpu):
+    """A float B is quantised per tensor on the device with its scale kept
+    there (no host read-back), so the whole call, quantisation included,
+    captures and replays."""
+    case = cases.uniform_blocks(512, 1024, 256, 200, seed=17)
+    q = void_amd.quantize_void_tensor(cases.make_void_tensor(case, "cpu")).to(gpu)
+    bf = torch.from_numpy(case.b).to(gpu)
+    _capture_and_check(lambda: void_amd.void_spmm_int8(q, bf), _other(gpu))

@@ -256,7 +256,7 @@ def void_spmm_fp8(a: FP8VOIDTensor, b: torch.Tensor, output_dtype: torch.dtype =
     if float_b and not b.is_floating_point():
         raise TypeError(f"B must be float8_e4m3fn or a float tensor, got {b.dtype}")
     from .int_quant import _b_scale_args
-    scalar_scale, scale_vec = _b_scale_args(b_scale, N, b.device)
+    scalar_scale, scale_vec, _ = _b_scale_args(b_scale, N, b.device)
     if out is None:
         out = torch.empty(M, N, dtype=output_dtype, device=b.device)
     elif out.shape != (M, N) or out.dtype != output_dtype:

@@ -310,17 +310,22 @@ def dequantize_void_tensor(int8_tensor: Int8VOIDTensor):
         density=int8_tensor.n_blocks / max(n_br * n_bc, 1))
 
 
-def _b_scale_args(b_scale, N: int, device) -> Tuple[float, Optional[torch.Tensor]]:
-    """Split a B scale into (scalar, per-column tensor or None)."""
+def _b_scale_args(b_scale, N: int, device) -> Tuple[float, Optional[torch.Tensor], bool]:
+    """Split a B scale into (scalar, per-column tensor or None, per-column?).
+
+    A one-element tensor is a per-tensor scale: it reaches the kernel as N
+    copies on the device (the same products as the scalar, without reading
+    it back to the host, which would stall the stream and break graph
+    capture), and keeps the per-tensor defaults."""
     if b_scale is None:
-        return 1.0, None
+        return 1.0, None, False
     if isinstance(b_scale, torch.Tensor):
         if b_scale.numel() == 1 and b_scale.dim() <= 1 and N != 1:
-            return float(b_scale.reshape(()).item()), None
+            return 1.0, b_scale.reshape(1).to(device=device, dtype=torch.float32).expand(N).contiguous(), False
         if b_scale.numel() != N:
             raise ValueError(f"b_scale has {b_scale.numel()} entries, expected 1 or N={N}")
-        return 1.0, b_scale.reshape(-1).to(device=device, dtype=torch.float32).contiguous()
-    return float(b_scale), None
+        return 1.0, b_scale.reshape(-1).to(device=device, dtype=torch.float32).contiguous(), True
+    return float(b_scale), None, False
 
 
 def void_spmm_int8(
@@ -337,9 +342,10 @@ def void_spmm_int8(
 ) -> torch.Tensor:
     """INT8 block-sparse SpMM C = A @ B (int_quant.py:543-612) on the gfx950 kernel.
 
-    Reference behaviour kept: a float B is quantised per tensor (with a host
-    sync for the scale); an int8 B without b_scale uses 1.0; ``out`` is fully
-    overwritten; the default epilogue is the reference's row-mean scaling.
+    Reference behaviour kept: a float B is quantised per tensor (its scale
+    stays on the device: no host sync); an int8 B without b_scale uses 1.0;
+    ``out`` is fully overwritten; the default epilogue is the reference's
+    row-mean scaling.
 
     Additions (keyword-only, defaults preserve the reference):
       b_scale   may be a tensor of N per-column scales;
@@ -359,10 +365,11 @@ def void_spmm_int8(
     if b.dtype != torch.int8:
         cfg = IntQuantConfig(format=IntFormat.INT8, symmetric=True, scale_mode=ScaleMode.PER_TENSOR)
         b, params = quantize_tensor(b, cfg)
-        b_scale = params.scale.item()
-    scalar_scale, scale_vec = _b_scale_args(b_scale, N, b.device)
+        b_scale = params.scale.reshape(1)
+    scalar_scale, scale_vec, per_column = _b_scale_args(b_scale, N, b.device)
+    per_column = per_column and b_scale.numel() != 1 if isinstance(b_scale, torch.Tensor) else per_column
     if epilogue is None:
-        epilogue = "row_mean" if scale_vec is None else "per_block"
+        epilogue = "per_block" if per_column else "row_mean"
     if epilogue not in _lib.EPILOGUES:
         raise ValueError(f"unknown epilogue {epilogue!r}")
     if out_dtype is None:
