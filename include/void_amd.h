@@ -292,6 +292,15 @@ int void_spmm_bf16(const void_bsr_desc* a, const void_dense_args* d, const void_
 int void_spmm_f16(const void_bsr_desc* a, const void_dense_args* d, const void_plan* plan,
                   void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Per-tensor symmetric INT8 quantisation of n contiguous floats b (a float
+ * B operand), as quantize_tensor (void/int_quant.py:254-325) with qmin =
+ * -128, qmax = 127: *scale = max(max|b| / 128, 1e-8), q = clamp(rint(b /
+ * scale), -128, 127).  The scale stays in device memory (the reference reads
+ * it back to the host).  partials: device workspace of 1024 uint32.  b
+ * 16-byte aligned, q 4-byte aligned. */
+int void_quantize_b_i8(const float* b, int64_t n, int8_t* q, float* scale, uint32_t* partials,
+                       hipStream_t stream);
+
 /* dst[c * ld_dst + r] = src[r * ld_src + c] for a rows x cols byte matrix:
  * a column-major int8 or E4M3 B (src: its N columns of K bytes, ld_src
  * between columns; rows = N, cols = K) made row-major (dst: K x N,

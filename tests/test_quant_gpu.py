@@ -77,3 +77,31 @@ def test_public_api_device_matches_host(gpu):
                                   epilogue="raw_i32")
     A = oracle.Bsr(host.values.numpy(), host.scales.numpy(), case.block_rows, case.block_cols, (case.M, case.K))
     assert np.array_equal(out.cpu().numpy(), oracle.i8_acc(A, bq))
+
+
+@pytest.mark.parametrize("shape,kind", [((4096, 512), "normal"), ((1000, 37), "normal"), ((3, 5), "normal"),
+                                        ((256, 64), "ties"), ((128, 128), "zeros"), ((77, 1), "negmax"),
+                                        ((64, 300), "wide")])
+def test_device_b_per_tensor_bit_exact(gpu, shape, kind):
+    """void_quantize_b_i8 (a float B's per-tensor INT8 quantisation, on the
+    device) gives quantize_tensor's codes and scale bit for bit: scale =
+    max|b| / 128 clamped at 1e-8, rint of an IEEE division, clamped to
+    [-128, 127]; halfway quotients, an all-zero B, a negative extreme and
+    odd element counts (a tail after the 16-byte loads) included."""
+    from void_amd.int_quant import _quantize_b_per_tensor, quantize_tensor, IntQuantConfig, IntFormat, ScaleMode
+    g = torch.Generator().manual_seed(sum(shape))
+    b = torch.randn(shape, generator=g)
+    if kind == "ties":
+        b = (torch.randint(-300, 300, shape, generator=g).float() + 0.5) * (6.0 / 128)
+        b[0, 0] = 6.0  # max |b| = 6: quotients b / (6 / 128) land on halves
+    elif kind == "zeros":
+        b = torch.zeros(shape)
+    elif kind == "negmax":
+        b[5, 0] = -40.0
+    elif kind == "wide":
+        b = b * torch.exp2(torch.randint(-30, 30, shape, generator=g).float())
+    cfg = IntQuantConfig(format=IntFormat.INT8, symmetric=True, scale_mode=ScaleMode.PER_TENSOR)
+    ref_q, ref_p = quantize_tensor(b, cfg)
+    q, scale = _quantize_b_per_tensor(b.to(gpu))
+    assert torch.equal(q.cpu(), ref_q)
+    assert torch.equal(scale.cpu().view(torch.int32), ref_p.scale.reshape(1).view(torch.int32))

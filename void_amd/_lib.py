@@ -134,6 +134,7 @@ SIGNATURES = {
     "void_spmm_f16": (c_int, [POINTER(BsrDesc), POINTER(DenseArgs), POINTER(Plan),
                               c_void_p, c_size_t, c_void_p]),
     "void_transpose_b8": (c_int, [c_void_p, c_int64, c_int32, c_int32, c_void_p, c_int64, c_void_p]),
+    "void_quantize_b_i8": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]),
     "void_quantize_tiles_i8": (c_int, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p]),
     "void_quantize_tiles_fp8": (c_int, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     "void_sddmm_f32": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int32, c_int32,

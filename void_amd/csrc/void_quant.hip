@@ -12,6 +12,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include <cstdint>
 
 #include "void_amd.h"
@@ -143,6 +145,73 @@ int check_args(const float* tiles, int32_t n_tiles, const void* q, const float* 
   return 1;
 }
 
+// Per-tensor symmetric INT8 quantisation of a float B (int_quant.py:178-214,
+// 308-325 with qmin = -128, qmax = 127): scale = max(max |b| / 128, 1e-8),
+// q = clamp(rint(b / scale), -128, 127) with IEEE division.  Two launches:
+// the first writes one partial max |b| per workgroup (as bits: for the
+// non-negative floats the integer order is the float order, and a NaN's
+// bits exceed infinity's), the second reduces the partials in every
+// workgroup, quantises its share and has workgroup 0 write the scale.
+constexpr int kQbThreads = 256;
+constexpr int kQbMaxPartials = 1024;
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, uint32_t* red) {
+  v = wave_max_u32(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint32_t m = red[0];
+#pragma unroll
+  for (int w = 1; w < kQbThreads / 64; ++w) m = max(m, red[w]);
+  return m;
+}
+
+__global__ __launch_bounds__(kQbThreads) void b_amax_kernel(const float* __restrict__ b, int64_t n,
+                                                          uint32_t* __restrict__ partials) {
+  __shared__ uint32_t red[kQbThreads / 64];
+  typedef float v4f __attribute__((ext_vector_type(4)));
+  uint32_t m = 0;
+  const int64_t n4 = n / 4;
+  for (int64_t i = (int64_t)blockIdx.x * kQbThreads + threadIdx.x; i < n4; i += (int64_t)gridDim.x * kQbThreads) {
+    const v4f x = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(b) + i);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) m = max(m, __float_as_uint(x[k]) & 0x7fffffffu);
+  }
+  for (int64_t i = 4 * n4 + (int64_t)blockIdx.x * kQbThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kQbThreads)
+    m = max(m, __float_as_uint(b[i]) & 0x7fffffffu);
+  m = block_max_u32(m, red);
+  if (threadIdx.x == 0) partials[blockIdx.x] = m;
+}
+
+__global__ __launch_bounds__(kQbThreads) void b_quant_kernel(const float* __restrict__ b, int64_t n,
+                                                           const uint32_t* __restrict__ partials, int32_t n_partials,
+                                                           int8_t* __restrict__ q, float* __restrict__ scale_out) {
+  __shared__ uint32_t red[kQbThreads / 64];
+  typedef float v4f __attribute__((ext_vector_type(4)));
+  uint32_t m = 0;
+  for (int i = threadIdx.x; i < n_partials; i += kQbThreads) m = max(m, partials[i]);
+  m = block_max_u32(m, red);
+  const float scale = fmaxf(__uint_as_float(m) / 128.0f, 1e-8f);
+  if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = scale;
+  auto code = [&](float x) -> uint32_t {
+    const float r = __builtin_rintf(__fdiv_rn(x, scale));
+    return (uint32_t)(uint8_t)(int8_t)(int)fminf(fmaxf(r, -128.0f), 127.0f);
+  };
+  const int64_t n4 = n / 4;
+  for (int64_t i = (int64_t)blockIdx.x * kQbThreads + threadIdx.x; i < n4; i += (int64_t)gridDim.x * kQbThreads) {
+    const v4f x = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(b) + i);
+    const uint32_t w = code(x[0]) | (code(x[1]) << 8) | (code(x[2]) << 16) | (code(x[3]) << 24);
+    reinterpret_cast<uint32_t*>(q)[i] = w;
+  }
+  for (int64_t i = 4 * n4 + (int64_t)blockIdx.x * kQbThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kQbThreads)
+    q[i] = (int8_t)code(b[i]);
+}
+
 // dst[c][r] = src[r][c] for a rows x cols byte matrix (int8 or E4M3 codes):
 // a column-major B made row-major for the SpMM's LDS-DMA ring.  A workgroup
 // moves a 64-row x 256-column tile through LDS: 16-byte loads along the
@@ -184,6 +253,24 @@ __global__ __launch_bounds__(256) void transpose_b8_kernel(const uint8_t* __rest
 }  // namespace
 
 extern "C" {
+
+int void_quantize_b_i8(const float* b, int64_t n, int8_t* q, float* scale, uint32_t* partials,
+                       hipStream_t stream) {
+  void_internal_fail(VOID_OK, "");
+  if (n < 0) return void_internal_fail(VOID_ERR_ARG, "negative size");
+  if (n == 0) return VOID_OK;
+  if (!b || !q || !scale || !partials) return void_internal_fail(VOID_ERR_ARG, "null pointer");
+  if ((uintptr_t)b % 16 || (uintptr_t)q % 4) return void_internal_fail(VOID_ERR_ARG, "b must be 16-byte, q 4-byte aligned");
+  const int g = (int)std::min<int64_t>(kQbMaxPartials, std::max<int64_t>(1, (n + 4095) / 4096));
+  hipLaunchKernelGGL(b_amax_kernel, dim3(g), dim3(kQbThreads), 0, stream, b, n, partials);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return void_internal_fail(VOID_ERR_HIP, hipGetErrorString(e));
+  const int gq = (int)std::min<int64_t>(2048, std::max<int64_t>(1, (n + 4095) / 4096));
+  hipLaunchKernelGGL(b_quant_kernel, dim3(gq), dim3(kQbThreads), 0, stream, b, n, partials, g, q, scale);
+  e = hipGetLastError();
+  if (e != hipSuccess) return void_internal_fail(VOID_ERR_HIP, hipGetErrorString(e));
+  return VOID_OK;
+}
 
 int void_transpose_b8(const void* src, int64_t ld_src, int32_t rows, int32_t cols, void* dst, int64_t ld_dst,
                       hipStream_t stream) {

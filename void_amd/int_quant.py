@@ -328,6 +328,23 @@ def _b_scale_args(b_scale, N: int, device) -> Tuple[float, Optional[torch.Tensor
     return float(b_scale), None, False
 
 
+def _quantize_b_per_tensor(b: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """A float B quantised per tensor as the reference does (symmetric int8,
+    min-max scale), the scale left on the device: for a contiguous fp32 B
+    on the gfx950 kernels (void_quantize_b_i8), otherwise with quantize_tensor."""
+    if b.dtype == torch.float32 and b.is_contiguous() and b.data_ptr() % 16 == 0:
+        q = torch.empty(b.shape, dtype=torch.int8, device=b.device)
+        scale = torch.empty(1, dtype=torch.float32, device=b.device)
+        partials = torch.empty(1024, dtype=torch.int32, device=b.device)
+        st = _lib.lib().void_quantize_b_i8(b.data_ptr(), b.numel(), q.data_ptr(), scale.data_ptr(),
+                                           partials.data_ptr(), torch.cuda.current_stream(b.device).cuda_stream)
+        _lib.check(st, "void_quantize_b_i8")
+        return q, scale
+    cfg = IntQuantConfig(format=IntFormat.INT8, symmetric=True, scale_mode=ScaleMode.PER_TENSOR)
+    q, params = quantize_tensor(b, cfg)
+    return q, params.scale.reshape(1)
+
+
 def void_spmm_int8(
     a: Int8VOIDTensor,
     b: torch.Tensor,
@@ -363,9 +380,7 @@ def void_spmm_int8(
         raise ValueError(f"bias must be [{N}], got {tuple(bias.shape)}")
     _runtime.require_gpu(b, "B")
     if b.dtype != torch.int8:
-        cfg = IntQuantConfig(format=IntFormat.INT8, symmetric=True, scale_mode=ScaleMode.PER_TENSOR)
-        b, params = quantize_tensor(b, cfg)
-        b_scale = params.scale.reshape(1)
+        b, b_scale = _quantize_b_per_tensor(b)
     scalar_scale, scale_vec, per_column = _b_scale_args(b_scale, N, b.device)
     per_column = per_column and b_scale.numel() != 1 if isinstance(b_scale, torch.Tensor) else per_column
     if epilogue is None:
