@@ -33,6 +33,8 @@ def test_sddmm_tiles(gpu, M, K, N, n, seed, grouped, monkeypatch):
     from void_amd.format import build_bsr_layout
     if grouped in ("rows", "tile_rows"):
         monkeypatch.setenv("VOID_AMD_SDDMM", "rows")
+    elif grouped == "ring":  # the row-grouped ring even where the per-tile kernel would be chosen
+        monkeypatch.setenv("VOID_AMD_SDDMM", "grouped")
     if grouped == "tile_rows":
         grouped = None
     rng = np.random.default_rng(seed)
@@ -70,6 +72,8 @@ def test_sddmm_tiles_half_outputs(gpu, out_dtype, grouped, monkeypatch):
     from void_amd.format import build_bsr_layout
     if grouped in ("rows", "tile_rows"):
         monkeypatch.setenv("VOID_AMD_SDDMM", "rows")
+    elif grouped == "ring":  # the row-grouped ring even where the per-tile kernel would be chosen
+        monkeypatch.setenv("VOID_AMD_SDDMM", "grouped")
     if grouped == "tile_rows":
         grouped = None
     M, K, N = 640, 1024, 200

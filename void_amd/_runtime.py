@@ -520,8 +520,16 @@ def sddmm_tiles(grad_c: torch.Tensor, b: torch.Tensor, block_rows: torch.Tensor,
             return out
     g = grad_c.to(torch.float32).contiguous()
     bb = b.to(torch.float32).contiguous()
-    if layout is not None:
-        groups = layout.row_groups()
+    groups = layout.row_groups() if layout is not None else None
+    # Up to 1.5 row groups per CU: the per-tile kernel, whose workgroups
+    # always hold 8 tiles, outweighs the shared grad_c rows (c2, 262 groups of
+    # 6.3 tiles: 33.3 against 38.6 us; c3, 461 groups of 7.1: 44.9 against
+    # 40.5 us).  VOID_AMD_SDDMM=grouped / tiles forces one or the other.
+    force = os.environ.get("VOID_AMD_SDDMM")
+    if groups is not None and (force == "tiles" or (groups.shape[0] <= tuning.GFX950_CUS * 3 // 2
+                                                    and force not in ("grouped", "rows"))):
+        groups = None
+    if groups is not None:
         st = _lib.lib().void_sddmm_rows_f32(g.data_ptr(), g.stride(0), bb.data_ptr(), bb.stride(0), groups.data_ptr(),
                                             int(groups.shape[0]), layout.col_idx.data_ptr(), layout.order.data_ptr(),
                                             M, N, K, out.data_ptr(), out_code(out_dtype), stream)
