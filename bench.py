@@ -372,7 +372,7 @@ def bench_float(args, dev):
         cpu = {"value": round(ops / med / 1e12, 4), "unit": "TFLOP/s", "cores": len(os.sched_getaffinity(0)),
                "kind": "port", "ms": round(med * 1e3, 3),
                "sample": f"full {args.config} problem in fp32, torch CPU tile bmm + index_add, median of {len(times) - 1} reps"}
-    what = f"SDDMM backward of A (void_sddmm_rows_{args.dtype})" if args.op == "sddmm" else "BSpMM (void_spmm)"
+    what = "SDDMM backward of A (autograd's kernel choice)" if args.op == "sddmm" else "BSpMM (void_spmm)"
     dname = args.dtype
     line = {"metric": f"{dname.upper()} {what} effective TFLOP/s, {case.name} in {dname}", "value": round(tflops, 3),
             "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
