@@ -38,6 +38,14 @@ class DevicePlan:
     host_items: np.ndarray       # int32 [n_items, 32] copy, for inspection
     workspaces: Dict[Tuple[int, int], torch.Tensor] = field(default_factory=dict)
     ws_sizes: Dict[int, int] = field(default_factory=dict)  # N -> void_workspace_bytes
+    _cplan: Optional["_lib.Plan"] = None
+
+    def cplan(self) -> "_lib.Plan":
+        """The C descriptor of this plan (its arrays never change: built once)."""
+        if self._cplan is None:
+            self._cplan = _lib.Plan(items=self.items.data_ptr(), n_items=self.n_items,
+                                    n_split_tiles=self.n_split_tiles, n_slots=self.n_slots, chunk_tiles=self.chunk)
+        return self._cplan
 
     def workspace(self, N: int, device: torch.device,
                   stream: Optional[int] = None) -> Tuple[Optional[torch.Tensor], int]:
@@ -382,14 +390,13 @@ def launch(kind: str, dbsr: DeviceBsr, b: torch.Tensor, *, b_scale: float = 1.0,
     plan = dbsr.plan(chunk)
     stream = torch.cuda.current_stream(out.device).cuda_stream
     ws, ws_bytes = plan.workspace(N, out.device, stream)
-    cplan = _lib.Plan(items=plan.items.data_ptr(), n_items=plan.n_items,
-                      n_split_tiles=plan.n_split_tiles, n_slots=plan.n_slots, chunk_tiles=plan.chunk)
     if kind in ("int8", "fp8") and dbsr.use_row_groups(N):
         rg = dbsr.row_groups()
-        cplan.groups = rg.groups.data_ptr()
-        cplan.stages = rg.stages.data_ptr()
-        cplan.n_groups = rg.n_groups
-        cplan.max_group_stages = rg.max_stages
+        cplan = _lib.Plan(items=plan.items.data_ptr(), n_items=plan.n_items, n_split_tiles=plan.n_split_tiles,
+                          n_slots=plan.n_slots, chunk_tiles=plan.chunk, groups=rg.groups.data_ptr(),
+                          stages=rg.stages.data_ptr(), n_groups=rg.n_groups, max_group_stages=rg.max_stages)
+    else:
+        cplan = plan.cplan()
     dense = _lib.DenseArgs(
         b=b_t.data_ptr(), ldb=ldb, b_col_major=int(col_major), N=N, b_scale=float(b_scale),
         b_scale_vec=b_scale_vec.data_ptr() if b_scale_vec is not None else None,

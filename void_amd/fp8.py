@@ -273,10 +273,11 @@ def void_spmm_fp8(a: FP8VOIDTensor, b: torch.Tensor, output_dtype: torch.dtype =
     from .fusion import get_activation_code
     if bias is not None:
         bias = bias.to(device=b.device, dtype=torch.float32).contiguous()
-    chunk = chunk_tiles or tuning.select_chunk("fp8", a.n_blocks, N, a.device_bsr().max_row)
+    dbsr = a.device_bsr()
+    chunk = chunk_tiles or tuning.select_chunk("fp8", a.n_blocks, N, dbsr.max_row)
     act = get_activation_code(activation)
     if not float_b:
-        return _runtime.launch("fp8", a.device_bsr(), b.view(torch.uint8), b_scale=scalar_scale,
+        return _runtime.launch("fp8", dbsr, b.view(torch.uint8), b_scale=scalar_scale,
                                b_scale_vec=scale_vec, out=out, epilogue=_lib.EPI_PER_BLOCK, activation=act,
                                bias=bias, chunk=chunk)
     if chunk > tuning.FP32_B_MAX_CHUNK:
@@ -291,7 +292,7 @@ def void_spmm_fp8(a: FP8VOIDTensor, b: torch.Tensor, output_dtype: torch.dtype =
             kind = "fp8_bf16b" if b.dtype == torch.bfloat16 else "fp8_f16b"
             aligned = out.stride(1) == 1 and out.data_ptr() % 16 == 0 and out.stride(0) % 4 == 0
             tgt = out if aligned else torch.empty(M, N, dtype=output_dtype, device=b.device)
-            _runtime.launch(kind, a.device_bsr(), b16, b_scale=scalar_scale, b_scale_vec=scale_vec,
+            _runtime.launch(kind, dbsr, b16, b_scale=scalar_scale, b_scale_vec=scale_vec,
                             out=tgt, epilogue=_lib.EPI_PER_BLOCK, activation=act, bias=bias, chunk=chunk)
             if tgt is not out:
                 out.copy_(tgt)
@@ -303,13 +304,13 @@ def void_spmm_fp8(a: FP8VOIDTensor, b: torch.Tensor, output_dtype: torch.dtype =
         b32 = b.to(torch.float32).contiguous()
         if b32.data_ptr() % 16:
             b32 = b32.clone()
-        return _runtime.launch("fp8_f32b", a.device_bsr(), b32, b_scale=scalar_scale, b_scale_vec=scale_vec,
+        return _runtime.launch("fp8_f32b", dbsr, b32, b_scale=scalar_scale, b_scale_vec=scale_vec,
                                out=out, epilogue=_lib.EPI_PER_BLOCK, activation=act, bias=bias, chunk=chunk)
     b32 = torch.zeros(K, N4, dtype=torch.float32, device=b.device)
     b32[:, :N] = b
     pad = lambda v, fill: torch.cat([v, torch.full((N4 - N,), fill, dtype=v.dtype, device=v.device)])
     wide = torch.empty(M, N4, dtype=output_dtype, device=b.device)
-    _runtime.launch("fp8_f32b", a.device_bsr(), b32, b_scale=scalar_scale,
+    _runtime.launch("fp8_f32b", dbsr, b32, b_scale=scalar_scale,
                     b_scale_vec=None if scale_vec is None else pad(scale_vec, 1.0), out=wide,
                     epilogue=_lib.EPI_PER_BLOCK, activation=act, bias=None if bias is None else pad(bias, 0.0),
                     chunk=chunk)

@@ -406,7 +406,7 @@ def void_spmm_int8(
         raise ValueError(f"A on {a.values.device}, B on {b.device}")
     from .fusion import get_activation_code
     dbsr = a.device_bsr()
-    chunk = chunk_tiles or tuning.select_chunk("int8", a.n_blocks, N, a.device_bsr().max_row)
+    chunk = chunk_tiles or tuning.select_chunk("int8", a.n_blocks, N, dbsr.max_row)
     if bias is not None:
         bias = bias.to(device=b.device, dtype=torch.float32).contiguous()
     return _runtime.launch("int8", dbsr, b, b_scale=scalar_scale, b_scale_vec=scale_vec, out=out,
