@@ -92,3 +92,31 @@ def test_random_fp8(gpu, kernel, seed):
     bound = oracle.fp8_spmm(Aabs, bq & 0x7F, abs(bs))
     err = np.abs(out.cpu().numpy().astype(np.float64) - ref)
     assert np.all(err <= FP8_TOL * bound + 1e-30), (case.M, case.K, case.N)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_fp8_float_b(gpu, seed, monkeypatch):
+    """E4M3 tiles times a float B kept as given (fp32, bf16 or fp16 by seed),
+    on random ragged shapes, each ring shape in turn; the float64 oracle of
+    the reference's upcast semantics (fp8.py:624-671) is the bar."""
+    ring = (None, "cgd", "cgdk")[seed % 3]
+    if ring:
+        monkeypatch.setenv("VOID_AMD_KERNEL", ring)
+    else:
+        monkeypatch.delenv("VOID_AMD_KERNEL", raising=False)
+    case, rng = _case(seed)
+    dtype = (torch.float32, torch.bfloat16, torch.float16)[seed % 3 if seed % 2 else (seed // 2) % 3]
+    print(f"fp8 float-B seed={seed} M={case.M} K={case.K} N={case.N} {dtype}", flush=True)
+    f8 = void_amd.void_tensor_to_fp8(cases.make_void_tensor(case, "cpu"))
+    b = torch.from_numpy(case.b).to(dtype)
+    out = void_amd.void_spmm_fp8(f8.to(gpu), b.to(gpu), output_dtype=torch.float32)
+    A = oracle.Bsr(f8.values_fp8.view(torch.uint8).numpy(), f8.scaling_info.scale.numpy(),
+                   case.block_rows, case.block_cols, (case.M, case.K))
+    bf = b.float().numpy()
+    ref = oracle.fp8_spmm_float_b(A, bf)
+    Aabs = oracle.Bsr.__new__(oracle.Bsr)
+    Aabs.__dict__.update(A.__dict__)
+    Aabs.tiles = np.ascontiguousarray(A.tiles.view(np.uint8) & 0x7F)
+    bound = oracle.fp8_spmm_float_b(Aabs, np.abs(bf))
+    err = np.abs(out.cpu().numpy().astype(np.float64) - ref)
+    assert np.all(err <= FP8_TOL * bound + 1e-30), (case.M, case.K, case.N)
