@@ -387,3 +387,27 @@ def test_row_groups_not_planned_by_default(monkeypatch):
     assert not d.use_row_groups(128) and d._row_groups is None
     monkeypatch.setenv("VOID_AMD_KERNEL", "rg")
     assert not d.use_row_groups(128)
+
+
+def test_b_scale_args_keep_scales_on_the_device():
+    """A per-tensor B scale given as a tensor is never read back to the host:
+    it becomes N device copies with the per-tensor defaults kept."""
+    from void_amd.int_quant import _b_scale_args
+    s, v, per_col = _b_scale_args(torch.tensor([0.5]), 4, torch.device("cpu"))
+    assert s == 1.0 and per_col is False and torch.equal(v, torch.full((4,), 0.5))
+    s, v, per_col = _b_scale_args(torch.tensor([1.0, 2.0, 3.0]), 3, torch.device("cpu"))
+    assert per_col is True and torch.equal(v, torch.tensor([1.0, 2.0, 3.0]))
+    assert _b_scale_args(2.0, 7, torch.device("cpu")) == (2.0, None, False)
+    assert _b_scale_args(None, 7, torch.device("cpu")) == (1.0, None, False)
+    with pytest.raises(ValueError):
+        _b_scale_args(torch.ones(5), 4, torch.device("cpu"))
+
+
+def test_col_major_copy_rule(monkeypatch):
+    monkeypatch.delenv("VOID_AMD_BT", raising=False)
+    assert tuning.copy_col_major_b(14336, 4096)       # FFN config: tiles gather 112x B
+    assert not tuning.copy_col_major_b(1638, 4096)    # c2: 13x B, read in place
+    monkeypatch.setenv("VOID_AMD_BT", "0")
+    assert not tuning.copy_col_major_b(14336, 4096)
+    monkeypatch.setenv("VOID_AMD_BT", "1")
+    assert tuning.copy_col_major_b(1, 4096)
