@@ -39,7 +39,9 @@ from .fp8 import (
     FP8VOIDTensor,
     compute_amax,
     create_scaling_info,
+    dequantize_fp8_fused,
     dequantize_from_fp8,
+    quantize_fp8_fused,
     quantize_to_fp8,
     void_spmm_fp8,
     void_tensor_to_fp8,

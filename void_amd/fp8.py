@@ -127,6 +127,41 @@ def dequantize_from_fp8(tensor: torch.Tensor, scaling_info: FP8ScalingInfo,
     return r.to(output_dtype)
 
 
+def _scale_index(n: int, scales: torch.Tensor, per_tensor: bool) -> Optional[torch.Tensor]:
+    """Scale of each flat element: one for the tensor, or consecutive runs of
+    n // len(scales) elements per scale (the reference's elements_per_scale)."""
+    if per_tensor:
+        return None
+    eps = n // scales.numel()
+    return torch.arange(n, device=scales.device) // max(eps, 1)
+
+
+def quantize_fp8_fused(tensor: torch.Tensor, scaling_info: FP8ScalingInfo) -> torch.Tensor:
+    """FP8 quantisation with precomputed scales (fp8.py:350-388): fl(x *
+    scale_inv) clamped to +-max, rounded to E4M3 (the reference's kernel
+    stores E4M3 whatever the configured format); the amax history is not
+    updated.  Elementwise torch ops, like the reference's other host-side
+    quantisers here."""
+    cfg = scaling_info.config
+    flat = tensor.reshape(-1).to(torch.float32)
+    inv = scaling_info.scale_inv.to(device=flat.device, dtype=torch.float32).reshape(-1)
+    idx = _scale_index(flat.numel(), inv, cfg.scale_mode == "per_tensor")
+    scaled = flat * (inv[0] if idx is None else inv[idx.clamp_max(inv.numel() - 1)])
+    q = torch.clamp(scaled, -cfg.max_value, cfg.max_value).to(torch.float8_e4m3fn)
+    return q.view(tensor.shape)
+
+
+def dequantize_fp8_fused(tensor: torch.Tensor, scaling_info: FP8ScalingInfo,
+                         output_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """fp32(x) * scale in output_dtype (fp8.py:391-431), per tensor or per
+    run of elements."""
+    flat = tensor.reshape(-1).to(torch.float32)
+    sc = scaling_info.scale.to(device=flat.device, dtype=torch.float32).reshape(-1)
+    idx = _scale_index(flat.numel(), sc, scaling_info.config.scale_mode == "per_tensor")
+    r = flat * (sc[0] if idx is None else sc[idx.clamp_max(sc.numel() - 1)])
+    return r.to(output_dtype).view(tensor.shape)
+
+
 @dataclass
 class FP8VOIDTensor:
     """VOID tensor with FP8 tiles (fp8.py:438-570)."""
