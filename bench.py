@@ -164,11 +164,11 @@ def build_problem(cfg: str, dev, epilogue):
         bt = bq_t.to(dev)
         gelu = cfg == "c5"
         ep = epilogue or ("row_mean" if cfg == "c1" else "per_block")
-        out_dtype = torch.bfloat16 if gelu else torch.float32
+        out_dtype = torch.int32 if ep == "raw_i32" else torch.bfloat16 if gelu else torch.float32
         out = torch.empty(M, N, dtype=out_dtype, device=dev)
 
         def run():
-            if gelu:
+            if gelu and ep != "raw_i32":
                 return void_amd.void_spmm_gelu(qd, bt, b_scale=st, out=out, out_dtype=torch.bfloat16,
                                                epilogue=ep)
             return void_amd.void_spmm_int8(qd, bt, b_scale=st, out=out, epilogue=ep, chunk_tiles=prob.get("chunk"))
