@@ -234,6 +234,24 @@ def test_c5_row_group_kernel_full(gpu, monkeypatch):
     assert np.all(err <= 2.0 ** -8 * np.abs(ref) + 1e-4), err.max()
 
 
+@pytest.mark.parametrize("per_column", [False, True])
+@pytest.mark.parametrize("chunk", [None, 16, 200])
+def test_row_mean_rows_beyond_64_tiles(gpu, chunk, per_column, kernel):
+    """Block-rows of 65-96 tiles: the row-mean scale sum runs past the 64
+    scales a workgroup holds one per lane, and (chunk 16) split rows fold the
+    whole row from every chunk."""
+    case = cases.uniform_blocks(160, 3072, 256, 430, seed=11)
+    qd, A, bq, bs = _int8_setup(case, gpu, b_per_column=per_column)
+    assert np.diff(A.row_ptr).max() > 64
+    bt = torch.from_numpy(bq).to(gpu)
+    st = torch.from_numpy(bs).to(gpu) if per_column else float(bs)
+    acc = oracle.i8_acc(A, bq)
+    rm = void_amd.void_spmm_int8(qd, bt, b_scale=st, epilogue="row_mean", chunk_tiles=chunk)
+    torch.cuda.synchronize()
+    ref = oracle.row_mean(A, acc, bs)
+    assert np.array_equal(rm.cpu().numpy().view(np.int32), ref.view(np.int32))
+
+
 @pytest.mark.parametrize("chunk", [1, 3, 8, 100])
 def test_forced_split_row_mean_and_per_block(gpu, chunk, kernel):
     case = cases.uniform_blocks(1024, 2048, 256, 900, seed=3)
