@@ -236,8 +236,8 @@ def test_c5_row_group_kernel_full(gpu, monkeypatch):
 
 @pytest.mark.parametrize("per_column", [False, True])
 @pytest.mark.parametrize("chunk", [None, 16, 200])
-def test_row_mean_rows_beyond_64_tiles(gpu, chunk, per_column, kernel):
-    """Block-rows of 65-96 tiles: the row-mean scale sum runs past the 64
+def test_epilogues_rows_beyond_64_tiles(gpu, chunk, per_column, kernel):
+    """Block-rows of 65-96 tiles, every epilogue: the row-mean scale sum runs past the 64
     scales a workgroup holds one per lane, and (chunk 16) split rows fold the
     whole row from every chunk."""
     case = cases.uniform_blocks(160, 3072, 256, 430, seed=11)
@@ -247,9 +247,14 @@ def test_row_mean_rows_beyond_64_tiles(gpu, chunk, per_column, kernel):
     st = torch.from_numpy(bs).to(gpu) if per_column else float(bs)
     acc = oracle.i8_acc(A, bq)
     rm = void_amd.void_spmm_int8(qd, bt, b_scale=st, epilogue="row_mean", chunk_tiles=chunk)
+    raw = void_amd.void_spmm_int8(qd, bt, b_scale=st, epilogue="raw_i32", chunk_tiles=chunk)
+    pb = void_amd.void_spmm_int8(qd, bt, b_scale=st, epilogue="per_block", chunk_tiles=chunk)
     torch.cuda.synchronize()
     ref = oracle.row_mean(A, acc, bs)
     assert np.array_equal(rm.cpu().numpy().view(np.int32), ref.view(np.int32))
+    assert np.array_equal(raw.cpu().numpy(), acc)
+    refpb = oracle.i8_per_block(A, bq, bs)
+    assert np.all(np.abs(pb.cpu().numpy() - refpb) <= 1e-5 * _abs_bound(A, bq, bs) + 1e-30)
 
 
 @pytest.mark.parametrize("chunk", [1, 3, 8, 100])
