@@ -149,6 +149,27 @@ def test_c3_fp8_full(gpu, kernel, out_dtype):
     assert np.all(err <= lim), (err / lim).max()
 
 
+@pytest.mark.parametrize("chunk", [None, 16])
+def test_fp8_rows_beyond_64_tiles(gpu, kernel, chunk):
+    """E4M3 block-rows of 65-96 tiles (per-block scales past the 64 a
+    workgroup holds one per lane; chunk 16 splits them)."""
+    case = cases.uniform_blocks(160, 3072, 256, 430, seed=12)
+    f8 = void_amd.void_tensor_to_fp8(cases.make_void_tensor(case, "cpu"))
+    bq, bs = oracle.quantize_fp8_tensor(case.b)
+    A = oracle.Bsr(f8.values_fp8.view(torch.uint8).numpy(), f8.scaling_info.scale.numpy(),
+                   case.block_rows, case.block_cols, (case.M, case.K))
+    assert np.diff(A.row_ptr).max() > 64
+    Aabs = oracle.Bsr.__new__(oracle.Bsr)
+    Aabs.__dict__.update(A.__dict__)
+    Aabs.tiles = np.ascontiguousarray(A.tiles.view(np.uint8) & 0x7F)
+    ref, bound = oracle.fp8_spmm(A, bq, bs), oracle.fp8_spmm(Aabs, bq & 0x7F, abs(bs))
+    bt = torch.from_numpy(bq).to(gpu).view(torch.float8_e4m3fn)
+    out = void_amd.void_spmm_fp8(f8.to(gpu), bt, output_dtype=torch.float32, b_scale=float(bs), chunk_tiles=chunk)
+    torch.cuda.synchronize()
+    err = np.abs(out.cpu().numpy().astype(np.float64) - ref)
+    assert np.all(err <= FP8_TOL * bound + 1e-30), (err / (FP8_TOL * bound + 1e-30)).max()
+
+
 def test_fp8_default_output_is_fp16(gpu):
     """void_spmm_fp8 without output_dtype writes float16, as the reference."""
     case = cases.uniform_blocks(256, 512, 96, 40, seed=4)
