@@ -39,11 +39,47 @@ INT8_PEAK_TOPS = 5000.0   # dense MFMA int8, MI355X
 FP8_PEAK_TFLOPS = 5000.0  # dense MFMA fp8, MI355X
 BF16_PEAK_TFLOPS = 2500.0  # dense MFMA bf16, MI355X
 
-# Per-launch HBM traffic (bytes) of the SpMM measured with rocprofv3 --pmc
-# FETCH_SIZE and WRITE_SIZE in separate runs of `bench.py --counters`, each
-# scaled by what the same counter reads for a plain 64 MiB copy (FETCH x 1.9993,
-# WRITE x 1.0).  Workloads not listed here report null.
-MEASURED_TRAFFIC = {"c2": 19682436, "c3": 22283060, "c4": 91217453, "c5": 186818873}
+# Per-launch memory traffic of the SpMM kernels, measured with rocprofv3 PMC
+# passes over `bench.py --counters` and summarised by `bench.py
+# --traffic-summary` into this file (with the commit and the kernel source's
+# hash it was measured on).  A summary of other kernel source reports null.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+KERNEL_SOURCES = ("void_amd/csrc/void_spmm.hip", "void_amd/csrc/lds_dma.h")
+
+
+def kernel_source_sha() -> str:
+    import hashlib
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(cfg: str):
+    """(bytes per launch, provenance) of a config from the traffic summary, or
+    (None, reason) when there is none for the current kernel source."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            summ = json.load(fh)
+    except (OSError, ValueError):
+        return None, "no traffic summary"
+    ent = summ.get("configs", {}).get(cfg)
+    if ent is None:
+        return None, f"{cfg} not in the traffic summary"
+    src = {"file": os.path.relpath(TRAFFIC_FILE, ROOT), "commit": summ.get("commit"),
+           "kernel_source_sha": summ.get("kernel_source_sha"), "counters": summ.get("counters")}
+    if summ.get("kernel_source_sha") != kernel_source_sha():
+        return None, dict(src, stale="kernel source changed since the measurement")
+    return ent["traffic_bytes"], src
+
+
+def gather_bytes(prob) -> int:
+    """Bytes the column-group kernel moves from L2 into LDS per launch: every
+    (nonzero tile, 128-column panel) pair stages its A tile (1024 elements)
+    and its 32-row B slab (32 x 128 elements)."""
+    n_panels = -(-prob["N"] // 128)
+    return prob["nb"] * n_panels * (1024 * prob["a_esz"] + 32 * 128 * prob["b_esz"])
 
 
 def parse():
@@ -68,6 +104,8 @@ def parse():
     ap.add_argument("--chunk", type=int, default=None, help="override the Stream-K chunk")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline budget (0 = skip)")
     ap.add_argument("--profile", action="store_true", help="no CPU leg, no flush: for rocprofv3 runs")
+    ap.add_argument("--traffic-summary", default=None, metavar="PMC_DIR",
+                    help="summarise the rocprofv3 counter passes under PMC_DIR into profiles/hbm_traffic.json")
     ap.add_argument("--counters", action="store_true",
                     help="eager launches for rocprofv3 --pmc: each step overwrites 1 GiB, copies a "
                          "64 MiB calibration buffer, then runs the SpMM; prints no JSON line")
@@ -110,10 +148,11 @@ def build_problem(cfg: str, dev, epilogue):
         def run():
             return void_amd.void_spmm_fp8(f8, bt, output_dtype=torch.float16, out=out)
 
-        # Each product runs as two bf16 MFMA products (B's hi and lo halves),
-        # so the effective peak is half the bf16 one.
+        # Rated against the bf16 MFMA peak the kernel runs on (each product
+        # takes two bf16 MFMA products, B's hi and lo halves: that is the
+        # design's cost, not the roofline's), or HBM, whichever bounds it.
         prob.update(kind="fp8", dtype="fp8e4m3 x f32 (bf16 hi/lo)", out_bytes=2, b_scale_bytes=0, run=run,
-                    peak_ops=BF16_PEAK_TFLOPS / 2, epilogue="per_block", b_bytes=4 * K * N,
+                    peak_ops=BF16_PEAK_TFLOPS, epilogue="per_block", b_bytes=4 * K * N, b_esz=4,
                     workload=case.name.replace("c3_fp8", "c3f_fp8_float_b"))
         a_scales = f8.scaling_info.scale.cpu().numpy()
         tiles_f = f8.values_fp8.float().cpu()
@@ -127,7 +166,7 @@ def build_problem(cfg: str, dev, epilogue):
             return void_amd.void_spmm_fp8(f8, bt, output_dtype=torch.float16, out=out)
 
         prob.update(kind="fp8", dtype="fp8e4m3 x bf16", out_bytes=2, b_scale_bytes=0, run=run,
-                    peak_ops=BF16_PEAK_TFLOPS, epilogue="per_block", b_bytes=2 * K * N,
+                    peak_ops=BF16_PEAK_TFLOPS, epilogue="per_block", b_bytes=2 * K * N, b_esz=2,
                     workload=case.name.replace("c3_fp8", "c3h_fp8_bf16_b"))
         a_scales = f8.scaling_info.scale.cpu().numpy()
         tiles_f = f8.values_fp8.float().cpu()
@@ -180,6 +219,8 @@ def build_problem(cfg: str, dev, epilogue):
         tiles_f = q.values.float()
         b_deq = torch.from_numpy(bq.astype(np.float32) * bsv[None, :])
     prob.setdefault("workload", case.name)
+    prob.setdefault("a_esz", 1)
+    prob.setdefault("b_esz", 1)
     prob["ops"] = 2.0 * nb * 32 * 32 * N
     prob["bytes"] = (nb * 1024 + 4 * nb + 4 * nb + 4 * (nbr + 1) + prob["b_bytes"]
                      + prob["b_scale_bytes"] + M * N * prob["out_bytes"])
@@ -504,7 +545,7 @@ def roofline_of(prob, t_ms: float, cfg: str) -> dict:
     else:
         roof = {"bound": "mfma", "achieved": round(tops, 2), "peak": prob["peak_ops"], "unit": "TFLOP/s",
                 "frac": round(tops / prob["peak_ops"], 4)}
-    roof["traffic"] = MEASURED_TRAFFIC.get(cfg)
+    roof["traffic"], roof["traffic_source"] = measured_traffic(cfg)
     roof["algorithmic_bytes"] = prob["bytes"]
     roof["roofline_ms"] = round(max(t_roof_mem, t_roof_ops) * 1e3, 5)
     return roof
@@ -534,7 +575,8 @@ def per_config_line(cfg: str, dev, args) -> dict:
     res = {"workload": prob["workload"], "kind": prob["kind"], "dtype": prob["dtype"], "ms": round(cold, 5),
            "hot_ms": round(hot, 5), "tops": round(prob["ops"] / (cold * 1e-3) / 1e12, 3),
            "bound": roof["bound"], "frac": roof["frac"], "peak": roof["peak"], "roofline_ms": roof["roofline_ms"],
-           "traffic_ratio": (round(roof["traffic"] / prob["bytes"], 3) if roof["traffic"] else None)}
+           "traffic_ratio": (round(roof["traffic"] / prob["bytes"], 3) if roof["traffic"] else None),
+           "gather_bytes": gather_bytes(prob), "gather_tbs": round(gather_bytes(prob) / (cold * 1e-3) / 1e12, 2)}
     if args.cpu_seconds > 0:
         c = cpu_leg(prob, min(args.cpu_seconds, 3.0), cfg)
         res.update(cpu_ms=c["ms"], cpu_tops=c["value"], cpu_cores=c["cores"])
@@ -543,12 +585,12 @@ def per_config_line(cfg: str, dev, args) -> dict:
     return res
 
 
-def bench_floor(args, dev):
+def floor_measure(dev, steps: int, warmup: int) -> dict:
     """Practical floor for c2 in the same graph-and-flush harness: a launch of
     a tiny kernel (the fixed cost of one dispatch after the 1 GiB overwrite)
     and plain device copies moving c2's algorithmic bytes: all of them
     (read + write = 12.18 MB) and the SpMM's own split (3.8 MB read and
-    8.4 MB written are bounded by the larger, so a copy of the output size
+    8.4 MB written are bounded by the larger, so a fill of the output size
     shows the write side alone)."""
     import torch
     n_alg = 12178740  # c2's algorithmic bytes per launch
@@ -560,9 +602,14 @@ def bench_floor(args, dev):
     for name, fn, nbytes in (("tiny_kernel", lambda: tiny.fill_(1.0), 256),
                              ("copy_c2_bytes", lambda: half_dst.copy_(half), 2 * half.numel() * 4),
                              ("write_c2_output", lambda: c_out.fill_(2.0), c_out.numel() * 4)):
-        cold, hot, _ = time_gpu({"run": fn}, args.steps, args.warmup, flush=True)
+        cold, hot, _ = time_gpu({"run": fn}, steps, warmup, flush=True)
         res[name] = {"ms": round(cold, 5), "hot_ms": round(hot, 5), "bytes": nbytes,
                      "gbs": round(nbytes / (cold * 1e-3) / 1e9, 1)}
+    return res
+
+
+def bench_floor(args, dev):
+    res = floor_measure(dev, args.steps, args.warmup)
     line = {"metric": "practical floor for c2 (cold graph-and-flush harness)", "value": res["copy_c2_bytes"]["ms"],
             "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": res["copy_c2_bytes"]["ms"], "higher_is_better": False, "scaling": "weak",
@@ -575,8 +622,81 @@ def bench_floor(args, dev):
     print(json.dumps(line), flush=True)
 
 
+# Counter passes the traffic summary reads, one rocprofv3 run per pass (the
+# two DRAM counters share one pass; FETCH_SIZE and WRITE_SIZE take one each):
+#   rocprofv3 --pmc <counters> -d <pmc_dir>/pmc_<cfg>_<pass> -o run --output-format csv -- \
+#       python bench.py --config <cfg> --counters --steps 5
+TRAFFIC_COUNTERS = ("TCC_EA0_RDREQ_DRAM_32B_sum", "TCC_EA0_WRREQ_WRITE_DRAM_32B_sum", "FETCH_SIZE", "WRITE_SIZE")
+TRAFFIC_CONFIGS = ("c2", "c3", "c4", "c5")
+
+
+def traffic_summary(pmc_dir: str) -> None:
+    """Summarise the counter passes under pmc_dir into profiles/hbm_traffic.json.
+
+    Each pass's CSV holds, per step, the 64 MiB calibration copy and the SpMM.
+    A counter's value per dispatch is the mean over the steps after the first;
+    it is scaled by the copy's reading against the copy's known byte count
+    (64 MiB read, 64 MiB written).  DRAM_32B counters count 32-byte units of
+    L2 requests to device memory, which the Infinity Cache may serve; FETCH_SIZE
+    and WRITE_SIZE are in KiB."""
+    import csv
+    import glob
+    import subprocess
+    copy_bytes = 64 << 20
+    unit = {"TCC_EA0_RDREQ_DRAM_32B_sum": 32.0, "TCC_EA0_WRREQ_WRITE_DRAM_32B_sum": 32.0,
+            "FETCH_SIZE": 1024.0, "WRITE_SIZE": 1024.0}
+    out = {"counters": list(TRAFFIC_COUNTERS), "kernel_source_sha": kernel_source_sha(), "configs": {}}
+    try:
+        out["commit"] = subprocess.run(["git", "-C", ROOT, "rev-parse", "--short", "HEAD"], capture_output=True,
+                                       text=True).stdout.strip() or None
+    except OSError:
+        out["commit"] = None
+    for cfg in TRAFFIC_CONFIGS:
+        ent = {}
+        for ctr in TRAFFIC_COUNTERS:
+            files = glob.glob(os.path.join(pmc_dir, f"pmc_{cfg}_*", "**", "*counter_collection.csv"), recursive=True)
+            rows = [r for fn in files for r in csv.DictReader(open(fn)) if r["Counter_Name"] == ctr]
+            # Per step, the SpMM dispatch and the copy dispatched just before it
+            # (setup copies earlier in the run are not steps).
+            disp = {}
+            for r in rows:
+                name = r["Kernel_Name"]
+                kind = "spmm" if "spmm" in name else "copy" if "copy" in name.lower() else None
+                if kind is not None:
+                    d = disp.setdefault(int(r["Dispatch_Id"]), [kind, 0.0])
+                    d[1] += float(r["Counter_Value"])
+            vals = {"spmm": [], "copy": []}
+            last_copy = None
+            for _, (kind, v) in sorted(disp.items()):
+                if kind == "copy":
+                    last_copy = v
+                elif last_copy is not None:
+                    vals["spmm"].append(v)
+                    vals["copy"].append(last_copy)
+                    last_copy = None
+            vals = {k: v[1:] for k, v in vals.items()}
+            if not vals["spmm"]:
+                continue
+            spmm = sum(vals["spmm"]) / len(vals["spmm"]) * unit[ctr]
+            copy = sum(vals["copy"]) / len(vals["copy"]) * unit[ctr]
+            scale = copy_bytes / copy if copy else None
+            ent[ctr] = {"raw_bytes": round(spmm), "copy_raw_bytes": round(copy),
+                        "scale": None if scale is None else round(scale, 4),
+                        "bytes": None if scale is None else round(spmm * scale)}
+        rd, wr = ent.get(TRAFFIC_COUNTERS[0]), ent.get(TRAFFIC_COUNTERS[1])
+        if rd and wr and rd["bytes"] is not None and wr["bytes"] is not None:
+            ent["traffic_bytes"] = rd["bytes"] + wr["bytes"]
+            out["configs"][cfg] = ent
+    with open(TRAFFIC_FILE, "w") as fh:
+        json.dump(out, fh, indent=1)
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
+    if args.traffic_summary:
+        traffic_summary(args.traffic_summary)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); every GPU box here has one "
               "GPU and the SpMM path is built and measured on a single MI355X.", file=sys.stderr)
@@ -631,6 +751,8 @@ def main():
                   "hot_tops": round(prob["ops"] / (hot * 1e-3) / 1e12, 3),
                   "hot_gbs": round(prob["bytes"] / (hot * 1e-3) / 1e9, 1),
                   "roofline_ms": roofline_ms,
+                  "gather_bytes": gather_bytes(prob),
+                  "gather_tbs": round(gather_bytes(prob) / (t_ms * 1e-3) / 1e12, 2),
                   "dense_equiv_tops": round(2.0 * prob["M"] * prob["K"] * prob["N"] / (t_ms * 1e-3) / 1e12, 2),
                   "wall_s": round(wall, 3),
                   "device": device_peaks()},
@@ -644,6 +766,12 @@ def main():
         del prob
         torch.cuda.empty_cache()
         line["extra"]["per_config"] = {c: per_config_line(c, dev, args) for c in PER_CONFIG}
+        # The harness floor measured in the same run: c2's time over a plain
+        # copy of its algorithmic bytes.
+        fl = floor_measure(dev, min(args.steps, 20), args.warmup)
+        line["extra"]["floor"] = fl
+        line["extra"]["c2_over_copy"] = round(t_ms / fl["copy_c2_bytes"]["ms"], 3)
+        line["extra"]["c2_over_tiny_kernel"] = round(t_ms / fl["tiny_kernel"]["ms"], 3)
     print(json.dumps(line), flush=True)
 
 

@@ -411,24 +411,3 @@ def test_col_major_copy_rule(monkeypatch):
     assert not tuning.copy_col_major_b(14336, 4096)
     monkeypatch.setenv("VOID_AMD_BT", "1")
     assert tuning.copy_col_major_b(1, 4096)
-
-
-def test_autotune_api_reports_the_fixed_configuration():
-    """The reference's autotuning names (autotune.py) answer with the one
-    gfx950 configuration: 32x32 tiles, 128-column panels, 4 waves, 2 stages."""
-    from void_amd import autotune
-    cfg = autotune.generate_spmm_configs(512, 32, 32)
-    assert cfg == [autotune.KernelConfig(TILE_M=32, TILE_K=32, TILE_N=128, num_warps=4, num_stages=2)]
-    assert autotune.KernelConfig.from_dict(cfg[0].to_dict()) == cfg[0] and hash(cfg[0]) == hash(cfg[0])
-    c = autotune.AutotuneCache()
-    assert c.make_key("spmm", 4096, 4000, 600, 32, 32) == "spmm_M4096_K2048_N512_TM32_TK32"
-    assert c.get("x") is None
-    c.set("x", cfg[0])
-    assert c.get("x") == cfg[0]
-    vt = void_amd.dense_to_void(torch.zeros(64, 64))
-    assert autotune.autotune_spmm(vt, torch.zeros(64, 8)) == cfg[0]
-    autotune.clear_autotune_cache()
-    assert autotune._autotune_cache.cache == {}
-    assert [void_amd.compute_optimal_tile_n(n) for n in (1, 3, 8, 16, 40, 64, 100, 128, 4096)] == \
-        [1, 4, 8, 16, 32, 64, 64, 128, 128]
-    assert void_amd.MIN_TENSOR_CORE_K == 16

@@ -134,30 +134,3 @@ def test_float_empty_and_reference_defaults(gpu):
     out2 = void_amd.void_spmm(vt2, torch.from_numpy(B).to(gpu))
     ref2 = A.toarray().astype(np.float64) @ B.astype(np.float64)
     assert np.all(np.abs(out2.cpu().numpy() - ref2) <= _bound(vt2, B) + 1e-30)
-
-
-def test_reference_float_entry_points(gpu):
-    """The reference's other float SpMM names: void_spmv (vector and [K, 1]
-    inputs), void_spmm_autotuned / _pipelined / _with_autotune (the same
-    kernel and bits as void_spmm) and void_spmm_work_stealing (the Stream-K
-    path on n_workers workers; deterministic)."""
-    case = cases.uniform_blocks(1000, 900, 64, 300, seed=23)
-    vt = cases.make_void_tensor(case, "cpu").to(gpu)
-    A = _dense_of(vt)
-    x = torch.from_numpy(case.b[:, 0].copy()).to(gpu)
-    y = void_amd.void_spmv(vt, x)
-    assert y.shape == (1000,) and y.dtype == torch.float32
-    n_row = 32 * int(np.bincount(case.block_rows).max())
-    xd = case.b[:, 0].astype(np.float64)
-    assert np.all(np.abs(y.cpu().numpy() - A @ xd) <= n_row * U * (np.abs(A) @ np.abs(xd)) + 1e-30)
-    y2 = void_amd.void_spmv(vt, x.reshape(-1, 1))
-    assert y2.shape == (1000, 1) and torch.equal(y2[:, 0], y)
-    out = torch.full((1000,), float("nan"), device=gpu)
-    assert void_amd.void_spmv(vt, x, out=out) is out and torch.equal(out, y)
-    B = torch.from_numpy(case.b).to(gpu)
-    ref = void_amd.void_spmm(vt, B)
-    for fn in (void_amd.void_spmm_autotuned, void_amd.void_spmm_pipelined, void_amd.void_spmm_with_autotune):
-        assert torch.equal(fn(vt, B), ref)
-    ws = void_amd.void_spmm_work_stealing(vt, B, n_workers=64)
-    assert torch.equal(ws, void_amd.void_spmm_work_stealing(vt, B, n_workers=64))
-    assert np.all(np.abs(ws.cpu().numpy() - A @ case.b.astype(np.float64)) <= _bound(vt, case.b) + 1e-30)

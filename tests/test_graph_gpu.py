@@ -144,3 +144,42 @@ def test_graph_int8_float_b(gpu):
     q = void_amd.quantize_void_tensor(cases.make_void_tensor(case, "cpu")).to(gpu)
     bf = torch.from_numpy(case.b).to(gpu)
     _capture_and_check(lambda: void_amd.void_spmm_int8(q, bf), _other(gpu))
+
+
+def test_graph_two_captures_of_one_split_plan(gpu):
+    """Two graphs captured from one split plan, the second replayed first and
+    then the two alternately: each capture owns a workspace zeroed inside
+    its own graph, so no replay depends on another graph's zeroing or shares
+    its arrival counters."""
+    case = cases.uniform_blocks(1024, 2048, 256, 900, seed=5)
+    q, bt, st = _int8(case, gpu)
+    fn = lambda: void_amd.void_spmm_int8(q, bt, b_scale=st, epilogue="per_block", chunk_tiles=3)
+    ref = fn()
+    torch.cuda.synchronize()
+    ref = ref.clone()
+    assert any(p.n_split_tiles > 0 for p in q.device_bsr().plans.values())
+    graphs, outs = [], []
+    for _ in range(2):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs.append(fn())
+        graphs.append(g)
+    torch.cuda.synchronize()
+    other = _other(gpu)
+    for k in (1, 0, 1, 0, 0, 1):
+        outs[k].zero_()
+        torch.cuda.synchronize()
+        graphs[k].replay()
+        other()
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(outs[k]), _bits(ref)), k
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for k, s in ((0, s1), (1, s2)):
+        outs[k].zero_()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s1):
+        graphs[0].replay()
+    with torch.cuda.stream(s2):
+        graphs[1].replay()
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(outs[0]), _bits(ref)) and torch.equal(_bits(outs[1]), _bits(ref))

@@ -105,3 +105,25 @@ def test_device_b_per_tensor_bit_exact(gpu, shape, kind):
     q, scale = _quantize_b_per_tensor(b.to(gpu))
     assert torch.equal(q.cpu(), ref_q)
     assert torch.equal(scale.cpu().view(torch.int32), ref_p.scale.reshape(1).view(torch.int32))
+
+
+def test_device_b_per_tensor_nan(gpu):
+    """A NaN in a float B makes quantize_tensor's scale NaN (torch.clamp keeps
+    NaN); the device quantiser keeps it too, so void_spmm_int8 with that B
+    gives NaN on every row that has tiles, as the reference's NaN scale does,
+    and zeros on empty rows."""
+    from void_amd.int_quant import _quantize_b_per_tensor, quantize_tensor, IntQuantConfig, IntFormat, ScaleMode
+    b = torch.randn(256, 64, generator=torch.Generator().manual_seed(11))
+    b[17, 3] = float("nan")
+    cfg = IntQuantConfig(format=IntFormat.INT8, symmetric=True, scale_mode=ScaleMode.PER_TENSOR)
+    _, ref_p = quantize_tensor(b, cfg)
+    assert torch.isnan(ref_p.scale).all()
+    _, scale = _quantize_b_per_tensor(b.to(gpu))
+    assert torch.isnan(scale.cpu()).all()
+    case = cases.uniform_blocks(128, 256, 64, 12, seed=3)
+    q = void_amd.quantize_void_tensor(cases.make_void_tensor(case, "cpu"))
+    out = void_amd.void_spmm_int8(q.to(gpu), b.to(gpu)).cpu()
+    has = np.zeros(4, bool)
+    has[np.unique(case.block_rows)] = True
+    rows = torch.from_numpy(np.repeat(has, 32))
+    assert torch.isnan(out[rows]).all() and (out[~rows] == 0).all()

@@ -1,8 +1,8 @@
 """The reference's fusion and FP8 tests, on the same inputs and at the same
 tolerances (tests/test_fusion.py:22-390, tests/test_fp8.py:209-238), run
-through this package.  Where the reference checks only a shape (sparse MLP,
-FusedSparseLinear, the create_* helpers) the output is also compared with a
-float64 dense restatement of the same layers built from the scipy inputs."""
+through this package.  Where the reference checks only a shape
+(FusedSparseLinear) the output is also compared with a float64 dense
+restatement of the same layer built from the scipy inputs."""
 
 import numpy as np
 import pytest
@@ -11,9 +11,8 @@ import torch
 
 import void_amd
 from void_amd import csr_to_void, void_spmm
-from void_amd.fusion import (ActivationType, FusedOpType, FusedSparseLinear, create_fused_spmm_gelu,
-                             create_fused_spmm_relu, create_sparse_mlp, fused_sparse_mlp, get_activation_code,
-                             void_spmm_gelu, void_spmm_relu, void_spmm_silu)
+from void_amd.fusion import (ActivationType, FusedSparseLinear, get_activation_code, void_spmm_gelu, void_spmm_relu,
+                             void_spmm_silu)
 
 pytestmark = pytest.mark.gpu
 
@@ -31,17 +30,6 @@ def _gelu64(x):
 
 _ACT64 = {"gelu": _gelu64, "relu": lambda x: np.maximum(x, 0.0), "silu": lambda x: x / (1.0 + np.exp(-x)),
           "none": lambda x: x}
-
-
-def _mlp64(x, w1, w2, act, b1=None, b2=None):
-    h = w1.toarray().astype(np.float64) @ x.T
-    if b1 is not None:
-        h += b1[:, None]
-    h = _ACT64[act](h)
-    y = w2.toarray().astype(np.float64) @ h
-    if b2 is not None:
-        y += b2[:, None]
-    return y.T
 
 
 # tests/test_fusion.py:38-124: each fused activation against void_spmm then torch.
@@ -72,65 +60,6 @@ def test_void_spmm_float_against_dense(gpu, small):
     out = void_spmm(vt, torch.from_numpy(B).to(gpu)).cpu().numpy().astype(np.float64)
     want = small.toarray().astype(np.float64) @ B
     assert np.abs(out - want).max() < 1e-4
-
-
-# tests/test_fusion.py:145-190
-def test_fused_op_helpers(gpu, small):
-    vt = csr_to_void(small, device="cuda")
-    x = torch.randn(256, 64, device=gpu)
-    g = create_fused_spmm_gelu(vt)
-    assert g.op_type == FusedOpType.SPMM_GELU
-    assert torch.equal(g(x), void_spmm_gelu(vt, x))
-    bias = torch.randn(64, device=gpu)
-    r = create_fused_spmm_relu(vt, bias)
-    assert r(x).shape == (256, 64)
-    assert torch.equal(r(x), void_spmm_relu(vt, x, bias))
-
-
-# tests/test_fusion.py:195-268 (shapes), plus values against float64.
-@pytest.mark.parametrize("act", ["gelu", "relu", "silu"])
-@pytest.mark.parametrize("with_bias", [False, True])
-def test_sparse_mlp(gpu, act, with_bias):
-    np.random.seed(42)
-    w1 = sparse.random(512, 256, density=0.1, format="csr", dtype=np.float32)
-    w2 = sparse.random(128, 512, density=0.1, format="csr", dtype=np.float32)
-    W1, W2 = csr_to_void(w1, device="cuda"), csr_to_void(w2, device="cuda")
-    rng = np.random.default_rng(1)
-    x = rng.standard_normal((32, 256)).astype(np.float32)
-    b1 = rng.standard_normal(512).astype(np.float32) if with_bias else None
-    b2 = rng.standard_normal(128).astype(np.float32) if with_bias else None
-    tb = (lambda v: None if v is None else torch.from_numpy(v).to(gpu))
-    y = fused_sparse_mlp(torch.from_numpy(x).to(gpu), W1, W2, activation=act, bias1=tb(b1), bias2=tb(b2))
-    assert y.shape == (32, 128)
-    want = _mlp64(x.astype(np.float64), w1, w2, act, b1, b2)
-    assert np.abs(y.cpu().numpy() - want).max() < 1e-4 * max(1.0, np.abs(want).max())
-
-
-# tests/test_fusion.py:371-390
-def test_create_sparse_mlp(gpu):
-    np.random.seed(42)
-    w1 = sparse.random(256, 128, density=0.1, format="csr", dtype=np.float32)
-    w2 = sparse.random(64, 256, density=0.1, format="csr", dtype=np.float32)
-    W1, W2 = csr_to_void(w1, device="cuda"), csr_to_void(w2, device="cuda")
-    op = create_sparse_mlp(W1, W2, activation="gelu")
-    assert op.op_type == FusedOpType.SPARSE_MLP and len(op.sparse_tensors) == 2 and op.activation == "gelu"
-    x = np.random.default_rng(2).standard_normal((16, 128)).astype(np.float32)
-    y = op(torch.from_numpy(x).to(gpu))
-    assert y.shape == (16, 64)
-    assert np.abs(y.cpu().numpy() - _mlp64(x.astype(np.float64), w1, w2, "gelu")).max() < 1e-4
-
-
-def test_create_sparse_mlp_second_bias_only(gpu):
-    """A lone bias2 goes to the second layer."""
-    np.random.seed(42)
-    w1 = sparse.random(256, 128, density=0.1, format="csr", dtype=np.float32)
-    w2 = sparse.random(64, 256, density=0.1, format="csr", dtype=np.float32)
-    b2 = np.random.default_rng(3).standard_normal(64).astype(np.float32)
-    op = create_sparse_mlp(csr_to_void(w1, device="cuda"), csr_to_void(w2, device="cuda"), "relu",
-                           bias2=torch.from_numpy(b2).to(gpu))
-    x = np.random.default_rng(4).standard_normal((16, 128)).astype(np.float32)
-    y = op(torch.from_numpy(x).to(gpu)).cpu().numpy()
-    assert np.abs(y - _mlp64(x.astype(np.float64), w1, w2, "relu", None, b2)).max() < 1e-4
 
 
 # tests/test_fusion.py:273-345 (shapes), plus values.

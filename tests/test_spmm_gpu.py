@@ -28,16 +28,15 @@ pytestmark = pytest.mark.gpu
 FP8_TOL = 2.0 ** -13
 
 
-@pytest.fixture(params=["cg", "cgd", "cgd3", "cgdk", "bsr", "rg"])
+@pytest.fixture(params=["cgd", "cgd3", "cgdk", "bsr", "rg"])
 def kernel(request, monkeypatch):
     """Runs a test on each SpMM kernel: the column-group kernel with its
     LDS-DMA ring of 4 tiles per stage (=cgd; column-major B runs the
-    register-staged loop), the 3-tile ring that unsplit grids beyond 512
-    workgroups take by default (=cgd3), the two-ring 8-wave workgroups that
-    grids of at most 512 workgroups and plans with split rows take (=cgdk),
-    the register-staged column-group loop (=cg), the
-    general kernel (=bsr) and the row-grouped kernel (=rg, where its
-    conditions hold; elsewhere the default dispatch runs)."""
+    register-staged loop, its only default use), the 3-tile ring that unsplit
+    grids beyond 512 workgroups take by default (=cgd3), the two-ring 8-wave
+    workgroups that grids of at most 512 workgroups and plans with split rows
+    take (=cgdk), the general kernel (=bsr) and the row-grouped kernel (=rg,
+    where its conditions hold; elsewhere the default dispatch runs)."""
     monkeypatch.setenv("VOID_AMD_KERNEL", request.param)
     return request.param
 
@@ -188,6 +187,42 @@ def test_c4_powerlaw_streamk_raw(gpu):
     plan = qd.device_bsr().plans
     assert any(p.n_split_tiles > 0 for p in plan.values()), "c4 must exercise split rows"
     assert np.array_equal(out.cpu().numpy(), oracle.i8_acc(A, bq))
+
+
+def test_c4_powerlaw_per_block_full(gpu, monkeypatch):
+    """Config 4 exactly as benched: per-block dequantisation into fp32 with
+    per-column B scales, on the default dispatch (rows split at the default
+    chunk, two-ring workgroups), checked over the whole 16384 x 256 output
+    against the oracle within 1e-5 of sum_t |s_t||A_t||B| |s_b|."""
+    monkeypatch.delenv("VOID_AMD_KERNEL", raising=False)
+    case = cases.c4_powerlaw()
+    qd, A, bq, bs = _int8_setup(case, gpu)
+    out = void_amd.void_spmm_int8(qd, torch.from_numpy(bq).to(gpu), b_scale=torch.from_numpy(bs).to(gpu),
+                                  epilogue="per_block")
+    torch.cuda.synchronize()
+    assert any(p.n_split_tiles > 0 for p in qd.device_bsr().plans.values()), "c4 must exercise split rows"
+    ref = oracle.i8_per_block(A, bq, bs)
+    bound = _abs_bound(A, bq, bs)
+    err = np.abs(out.cpu().numpy().astype(np.float64) - ref)
+    assert np.all(err <= 1e-5 * bound + 1e-30), (err / (bound + 1e-30)).max()
+
+
+def test_c5_ffn_full_every_row(gpu, monkeypatch):
+    """Config 5 exactly as benched (INT8 per-block, per-token scales, GELU
+    into bf16, default dispatch) over every one of its 448 block-rows: the
+    int32 accumulators bit-exact against the oracle, the GELU output within
+    one bf16 rounding plus 1e-4."""
+    monkeypatch.delenv("VOID_AMD_KERNEL", raising=False)
+    case = cases.c5_ffn()
+    qd, A, bq, bs = _int8_setup(case, gpu)
+    bt, st = torch.from_numpy(bq).to(gpu), torch.from_numpy(bs).to(gpu)
+    out = void_amd.void_spmm_gelu(qd, bt, b_scale=st, out_dtype=torch.bfloat16, epilogue="per_block")
+    raw = void_amd.void_spmm_int8(qd, bt, b_scale=st, epilogue="raw_i32")
+    torch.cuda.synchronize()
+    assert np.array_equal(raw.cpu().numpy(), oracle.i8_acc(A, bq))
+    ref = oracle.gelu_tanh(oracle.i8_per_block(A, bq, bs))
+    err = np.abs(out.float().cpu().numpy() - ref)
+    assert np.all(err <= 2.0 ** -8 * np.abs(ref) + 1e-4), err.max()
 
 
 def test_c5_ffn_full_sampled_rows(gpu, monkeypatch):

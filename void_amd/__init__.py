@@ -39,22 +39,17 @@ from .fp8 import (
     FP8VOIDTensor,
     compute_amax,
     create_scaling_info,
-    dequantize_fp8_fused,
     dequantize_from_fp8,
-    quantize_fp8_fused,
     quantize_to_fp8,
     void_spmm_fp8,
     void_tensor_to_fp8,
 )
-from .fusion import (ActivationType, FusedOpType, FusedSparseLinear, FusedSparseOp, create_fused_spmm_gelu,
-                     create_fused_spmm_relu, create_sparse_mlp, fused_sparse_mlp, get_activation_code, void_spmm_gelu,
-                     void_spmm_relu, void_spmm_silu)
+from .fusion import (ActivationType, FusedSparseLinear, get_activation_code, void_spmm_gelu, void_spmm_relu,
+                     void_spmm_silu)
 from .packed import load_packed, pack, save_packed, unpack
-from .ops import MIN_TENSOR_CORE_K, compute_optimal_tile_n, void_spmm, void_spmm_autotuned, void_spmm_pipelined, void_spmv
-from .autotune import KernelConfig, clear_autotune_cache, void_spmm_with_autotune
+from .ops import MIN_TENSOR_CORE_K, compute_optimal_tile_n, void_spmm
 from .autograd import SparseLinear, VOIDSpMM, VOIDSpMMFunction
-from .stream_k import (StreamKWorkload, analyze_workload_balance, compute_stream_k_workload, void_spmm_stream_k,
-                       void_spmm_work_stealing)
+from .stream_k import StreamKWorkload, analyze_workload_balance, compute_stream_k_workload, void_spmm_stream_k
 
 __version__ = "0.1.0"
 
@@ -68,6 +63,6 @@ __all__ = [
     "quantize_to_fp8", "dequantize_from_fp8", "void_spmm_fp8", "void_tensor_to_fp8",
     "ActivationType", "get_activation_code", "void_spmm_gelu", "void_spmm_relu", "void_spmm_silu",
     "StreamKWorkload", "compute_stream_k_workload", "analyze_workload_balance", "void_spmm_stream_k",
-    "void_spmm_work_stealing", "void_spmm", "void_spmv", "void_spmm_autotuned", "void_spmm_pipelined",
-    "compute_optimal_tile_n", "MIN_TENSOR_CORE_K", "KernelConfig", "clear_autotune_cache", "void_spmm_with_autotune",
+    "void_spmm", "compute_optimal_tile_n", "MIN_TENSOR_CORE_K", "FusedSparseLinear", "SparseLinear", "VOIDSpMM",
+    "VOIDSpMMFunction", "pack", "unpack", "save_packed", "load_packed",
 ]

@@ -12,7 +12,8 @@ from __future__ import annotations
 import ctypes
 import os
 from dataclasses import dataclass, field
-from typing import Dict, Optional, Tuple
+from collections import OrderedDict
+from typing import Dict, List, Optional, Tuple
 
 import numpy as np
 import torch
@@ -28,6 +29,11 @@ _OUT_CODES = {
 }
 
 
+# Streams whose eager split-row workspaces a plan keeps (least recently used
+# first out).
+MAX_STREAM_WORKSPACES = 8
+
+
 @dataclass
 class DevicePlan:
     items: torch.Tensor          # int32 [n_items, 32] on device (void_work_item)
@@ -36,7 +42,8 @@ class DevicePlan:
     n_slots: int
     chunk: int
     host_items: np.ndarray       # int32 [n_items, 32] copy, for inspection
-    workspaces: Dict[Tuple[int, int], torch.Tensor] = field(default_factory=dict)
+    workspaces: "OrderedDict[Tuple[int, int], torch.Tensor]" = field(default_factory=OrderedDict)
+    capture_workspaces: List[torch.Tensor] = field(default_factory=list)
     ws_sizes: Dict[int, int] = field(default_factory=dict)  # N -> void_workspace_bytes
     _cplan: Optional["_lib.Plan"] = None
 
@@ -55,12 +62,24 @@ class DevicePlan:
         blocks, so two launches that share one would mix their partials:
         each stream gets its own (launches on one stream run in order, and
         every launch leaves the counters at zero).  ``stream`` is the raw
-        stream handle, torch's current stream of ``device`` by default."""
+        stream handle, torch's current stream of ``device`` by default.
+
+        Eager launches reuse one workspace per stream, the last
+        ``MAX_STREAM_WORKSPACES`` streams being kept.  A launch under HIP graph
+        capture gets a workspace of its own, zeroed by a fill kernel captured
+        into the same graph, so that every graph clears and owns its counters
+        and graphs replayed on different streams never share them; it is kept
+        for the lifetime of the plan (one per capture)."""
         nbytes = self.ws_sizes.get(N)
         if nbytes is None:
             nbytes = self.ws_sizes[N] = int(_lib.lib().void_workspace_bytes(self.n_split_tiles, self.n_slots, N))
         if nbytes == 0:
             return None, 0
+        if torch.cuda.is_current_stream_capturing():
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            ws.zero_()
+            self.capture_workspaces.append(ws)
+            return ws, nbytes
         if stream is None:
             stream = torch.cuda.current_stream(device).cuda_stream
         key = (nbytes, int(stream))
@@ -71,6 +90,12 @@ class DevicePlan:
             ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
             _zero_on_stream(ws, int(stream), device)
             self.workspaces[key] = ws
+            while len(self.workspaces) > MAX_STREAM_WORKSPACES:
+                # The oldest stream's workspace is freed; the caching allocator
+                # keeps its memory until the work queued on that stream is done.
+                self.workspaces.popitem(last=False)
+        else:
+            self.workspaces.move_to_end(key)
         return ws, nbytes
 
 

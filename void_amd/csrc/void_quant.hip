@@ -196,7 +196,9 @@ __global__ __launch_bounds__(kQbThreads) void b_quant_kernel(const float* __rest
   uint32_t m = 0;
   for (int i = threadIdx.x; i < n_partials; i += kQbThreads) m = max(m, partials[i]);
   m = block_max_u32(m, red);
-  const float scale = fmaxf(__uint_as_float(m) / 128.0f, 1e-8f);
+  // torch.clamp(scale, min=1e-8) keeps a NaN scale (fmaxf would drop it).
+  const float amax = __uint_as_float(m) / 128.0f;
+  const float scale = amax != amax ? amax : fmaxf(amax, 1e-8f);
   if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = scale;
   auto code = [&](float x) -> uint32_t {
     const float r = __builtin_rintf(__fdiv_rn(x, scale));

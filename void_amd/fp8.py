@@ -127,41 +127,6 @@ def dequantize_from_fp8(tensor: torch.Tensor, scaling_info: FP8ScalingInfo,
     return r.to(output_dtype)
 
 
-def _scale_index(n: int, scales: torch.Tensor, per_tensor: bool) -> Optional[torch.Tensor]:
-    """Scale of each flat element: one for the tensor, or consecutive runs of
-    n // len(scales) elements per scale (the reference's elements_per_scale)."""
-    if per_tensor:
-        return None
-    eps = n // scales.numel()
-    return torch.arange(n, device=scales.device) // max(eps, 1)
-
-
-def quantize_fp8_fused(tensor: torch.Tensor, scaling_info: FP8ScalingInfo) -> torch.Tensor:
-    """FP8 quantisation with precomputed scales (fp8.py:350-388): fl(x *
-    scale_inv) clamped to +-max, rounded to E4M3 (the reference's kernel
-    stores E4M3 whatever the configured format); the amax history is not
-    updated.  Elementwise torch ops, like the reference's other host-side
-    quantisers here."""
-    cfg = scaling_info.config
-    flat = tensor.reshape(-1).to(torch.float32)
-    inv = scaling_info.scale_inv.to(device=flat.device, dtype=torch.float32).reshape(-1)
-    idx = _scale_index(flat.numel(), inv, cfg.scale_mode == "per_tensor")
-    scaled = flat * (inv[0] if idx is None else inv[idx.clamp_max(inv.numel() - 1)])
-    q = torch.clamp(scaled, -cfg.max_value, cfg.max_value).to(torch.float8_e4m3fn)
-    return q.view(tensor.shape)
-
-
-def dequantize_fp8_fused(tensor: torch.Tensor, scaling_info: FP8ScalingInfo,
-                         output_dtype: torch.dtype = torch.float16) -> torch.Tensor:
-    """fp32(x) * scale in output_dtype (fp8.py:391-431), per tensor or per
-    run of elements."""
-    flat = tensor.reshape(-1).to(torch.float32)
-    sc = scaling_info.scale.to(device=flat.device, dtype=torch.float32).reshape(-1)
-    idx = _scale_index(flat.numel(), sc, scaling_info.config.scale_mode == "per_tensor")
-    r = flat * (sc[0] if idx is None else sc[idx.clamp_max(sc.numel() - 1)])
-    return r.to(output_dtype).view(tensor.shape)
-
-
 @dataclass
 class FP8VOIDTensor:
     """VOID tensor with FP8 tiles (fp8.py:438-570)."""
@@ -333,14 +298,45 @@ def void_spmm_fp8(a: FP8VOIDTensor, b: torch.Tensor, output_dtype: torch.dtype =
                 out.copy_(tgt)
             return out
     # fp32 B, row-major with 16-byte aligned rows and N % 4 == 0 (the ring
-    # kernel's layout); other widths run on zero-padded columns.
+    # kernel's layout); other widths run on zero-padded columns.  The kernel
+    # addresses B and C with 31-bit byte offsets: a larger B or C runs in
+    # column slices that fit, each B slice copied contiguous and each result
+    # slice copied into place.
+    lim = 1 << 31
+    k_rows = (K + 31) // 32 * 32
+    esz = out.element_size()
+    width = N
+    if k_rows * ((N + 3) // 4 * 4) * 4 >= lim or M * ((N + 3) // 4 * 4) * esz >= lim:
+        width = min((lim - 1) // (k_rows * 4), (lim - 1) // max(M * esz, 1)) // 128 * 128
+        if width < 128:
+            raise ValueError(f"fp8 SpMM with an fp32 B: K={K} or M={M} too large for 31-bit offsets")
+    for n0 in range(0, N, width):
+        n1 = min(N, n0 + width)
+        whole = n0 == 0 and n1 == N
+        _launch_f32b(dbsr, b if whole else b[:, n0:n1], out if whole else None, output_dtype, scalar_scale,
+                     None if scale_vec is None else scale_vec[n0:n1], act, None if bias is None else bias[n0:n1],
+                     chunk, dst=out[:, n0:n1])
+    return out
+
+
+def _launch_f32b(dbsr, b: torch.Tensor, out: Optional[torch.Tensor], output_dtype: torch.dtype, scalar_scale: float,
+                 scale_vec: Optional[torch.Tensor], act: int, bias: Optional[torch.Tensor], chunk: int,
+                 dst: torch.Tensor) -> None:
+    """One E4M3 x fp32-B launch over B's columns, written to dst.  out, when
+    given, is dst itself and takes the result directly (N % 4 == 0)."""
+    K, N = b.shape
+    M = dst.shape[0]
     N4 = (N + 3) // 4 * 4
     if N4 == N:
         b32 = b.to(torch.float32).contiguous()
         if b32.data_ptr() % 16:
             b32 = b32.clone()
-        return _runtime.launch("fp8_f32b", dbsr, b32, b_scale=scalar_scale, b_scale_vec=scale_vec,
-                               out=out, epilogue=_lib.EPI_PER_BLOCK, activation=act, bias=bias, chunk=chunk)
+        tgt = out if out is not None else torch.empty(M, N, dtype=output_dtype, device=b.device)
+        _runtime.launch("fp8_f32b", dbsr, b32, b_scale=scalar_scale, b_scale_vec=scale_vec,
+                        out=tgt, epilogue=_lib.EPI_PER_BLOCK, activation=act, bias=bias, chunk=chunk)
+        if out is None:
+            dst.copy_(tgt)
+        return
     b32 = torch.zeros(K, N4, dtype=torch.float32, device=b.device)
     b32[:, :N] = b
     pad = lambda v, fill: torch.cat([v, torch.full((N4 - N,), fill, dtype=v.dtype, device=v.device)])
@@ -349,8 +345,7 @@ def void_spmm_fp8(a: FP8VOIDTensor, b: torch.Tensor, output_dtype: torch.dtype =
                     b_scale_vec=None if scale_vec is None else pad(scale_vec, 1.0), out=wide,
                     epilogue=_lib.EPI_PER_BLOCK, activation=act, bias=None if bias is None else pad(bias, 0.0),
                     chunk=chunk)
-    out.copy_(wide[:, :N])
-    return out
+    dst.copy_(wide[:, :N])
 
 
 def void_tensor_to_fp8(void_tensor, format: str = "e4m3", scale_mode: str = "per_block") -> FP8VOIDTensor:

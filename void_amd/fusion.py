@@ -10,21 +10,10 @@ of the INT8 or FP8 gfx950 kernel.  GELU is the tanh form of fusion.py:38-43.
 
 from __future__ import annotations
 
-from dataclasses import dataclass
 from enum import Enum
-from typing import List, Optional, Union
+from typing import Optional, Union
 
 import torch
-
-
-class FusedOpType(Enum):
-    """fusion.py:14-21."""
-    SPMM_GELU = "spmm_gelu"
-    SPMM_RELU = "spmm_relu"
-    SPMM_SILU = "spmm_silu"
-    SPMM_BIAS_GELU = "spmm_bias_gelu"
-    SPMM_BIAS_RELU = "spmm_bias_relu"
-    SPARSE_MLP = "sparse_mlp"
 
 
 class ActivationType(Enum):
@@ -159,58 +148,6 @@ def _void_spmm_activation_row_bias(a, b: torch.Tensor, bias: Optional[torch.Tens
     return float_spmm(a, b, out=out, bias=bias, activation=get_activation_code(activation), bias_per_row=True)
 
 
-def fused_sparse_mlp(x: torch.Tensor, w1, w2, activation: str = "gelu", bias1: Optional[torch.Tensor] = None,
-                     bias2: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """y = W2 @ activation(W1 @ x + b1) + b2 over the last axis of x
-    (fusion.py:559-600): two fused row-bias SpMMs on the fp32 kernel."""
-    x_2d = x.reshape(-1, x.shape[-1])
-    hidden = _void_spmm_activation_row_bias(w1, x_2d.T, bias1, None, activation)  # [hidden, batch]
-    out = _void_spmm_activation_row_bias(w2, hidden, bias2, None, "none")          # [out, batch]
-    return out.T.reshape(x.shape[:-1] + (out.shape[0],))
-
-
-@dataclass
-class FusedSparseOp:
-    """A fused sparse operation pattern (fusion.py:518-556)."""
-    op_type: FusedOpType
-    sparse_tensors: List
-    activation: Optional[str] = "gelu"
-    biases: Optional[List[torch.Tensor]] = None
-
-    def __call__(self, x: torch.Tensor) -> torch.Tensor:
-        bias = self.biases[0] if self.biases else None
-        if self.op_type in (FusedOpType.SPMM_GELU, FusedOpType.SPMM_BIAS_GELU):
-            return void_spmm_gelu(self.sparse_tensors[0], x, bias)
-        if self.op_type in (FusedOpType.SPMM_RELU, FusedOpType.SPMM_BIAS_RELU):
-            return void_spmm_relu(self.sparse_tensors[0], x, bias)
-        if self.op_type == FusedOpType.SPMM_SILU:
-            return void_spmm_silu(self.sparse_tensors[0], x, bias)
-        if self.op_type == FusedOpType.SPARSE_MLP:
-            return fused_sparse_mlp(x, self.sparse_tensors[0], self.sparse_tensors[1], activation=self.activation,
-                                    bias1=self.biases[0] if self.biases and len(self.biases) > 0 else None,
-                                    bias2=self.biases[1] if self.biases and len(self.biases) > 1 else None)
-        raise ValueError(f"Unknown fused op type: {self.op_type}")
-
-
-def create_fused_spmm_gelu(weight, bias: Optional[torch.Tensor] = None) -> FusedSparseOp:
-    """fusion.py:704-714."""
-    return FusedSparseOp(FusedOpType.SPMM_GELU, [weight], "gelu", [bias] if bias is not None else None)
-
-
-def create_fused_spmm_relu(weight, bias: Optional[torch.Tensor] = None) -> FusedSparseOp:
-    """fusion.py:717-727."""
-    return FusedSparseOp(FusedOpType.SPMM_RELU, [weight], "relu", [bias] if bias is not None else None)
-
-
-def create_sparse_mlp(w1, w2, activation: str = "gelu", bias1: Optional[torch.Tensor] = None,
-                      bias2: Optional[torch.Tensor] = None) -> FusedSparseOp:
-    """fusion.py:730-751.  The biases stay positional ([bias1, bias2], either
-    may be None): the reference compacts the list, which hands a lone bias2 to
-    the first layer."""
-    biases = None if bias1 is None and bias2 is None else [bias1, bias2]
-    return FusedSparseOp(FusedOpType.SPARSE_MLP, [w1, w2], activation, biases)
-
-
 class FusedSparseLinear(torch.nn.Module):
     """Sparse linear layer y = activation(W x + b) in one kernel
     (fusion.py:756-836): W is a float VOIDTensor [out_features, in_features],
@@ -283,6 +220,5 @@ class FusedSparseLinear(torch.nn.Module):
                 f"activation={self.activation}, bias={self.bias is not None}")
 
 
-__all__ = ["FusedOpType", "ActivationType", "FusedSparseOp", "FusedSparseLinear", "get_activation_code", "gelu_tanh",
-           "void_spmm_gelu", "void_spmm_relu", "void_spmm_silu", "fused_sparse_mlp", "create_fused_spmm_gelu",
-           "create_fused_spmm_relu", "create_sparse_mlp"]
+__all__ = ["ActivationType", "FusedSparseLinear", "get_activation_code", "gelu_tanh", "void_spmm_gelu",
+           "void_spmm_relu", "void_spmm_silu"]

@@ -128,33 +128,4 @@ def compute_optimal_tile_n(N: int) -> int:
     return 1 << max(0, (int(N) - 1).bit_length())
 
 
-def void_spmv(a, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """y = A @ x for a vector x of K entries, or [K, 1] (ops.py:291-353); y
-    has x's dtype and shape [M] (or [M, 1] for a [K, 1] x).  Runs as an SpMM
-    with one column."""
-    col = x.dim() == 2 and x.shape[1] == 1
-    if col:
-        x = x.squeeze(1)
-    if x.dim() != 1 or x.shape[0] != a.shape[1]:
-        raise ValueError(f"x must be [K={a.shape[1]}] or [K, 1], got {tuple(x.shape)}")
-    M = a.shape[0]
-    if out is not None and tuple(out.shape) != (M,):
-        raise ValueError(f"out must be [{M}]")
-    y = float_spmm(a, x.reshape(-1, 1), out=None if out is None else out.view(M, 1))
-    y = y.view(M) if out is None else out
-    return y.unsqueeze(1) if col else y
-
-
-def void_spmm_autotuned(a, b: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """The reference's autotuned SpMM (ops.py:441-491): the same gfx950 kernel as void_spmm."""
-    return void_spmm(a, b, out=out)
-
-
-def void_spmm_pipelined(a, b: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """The reference's software-pipelined SpMM (ops.py:612-): on gfx950 the
-    LDS-DMA ring of void_spmm is the pipelined kernel."""
-    return void_spmm(a, b, out=out)
-
-
-__all__ = ["void_spmm", "float_spmm", "void_spmv", "void_spmm_autotuned", "void_spmm_pipelined",
-           "compute_optimal_tile_n", "MIN_TENSOR_CORE_K"]
+__all__ = ["void_spmm", "float_spmm", "compute_optimal_tile_n", "MIN_TENSOR_CORE_K"]

@@ -146,14 +146,3 @@ def void_spmm_stream_k(a, b: torch.Tensor, workload: Optional[StreamKWorkload] =
 __all__ = ["StreamKWorkload", "compute_stream_k_workload", "analyze_workload_balance", "void_spmm_stream_k",
            "workload_plan"]
 
-
-def void_spmm_work_stealing(a, b: torch.Tensor, n_workers: int = 256,
-                            out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """The reference's work-stealing SpMM (stream_k.py:400-): its workers
-    take rows from an atomic counter.  Here the hardware dispatch of the
-    Stream-K work items does that balancing, so this is void_spmm_stream_k
-    on a workload of n_workers workers."""
-    if n_workers < 1:
-        raise ValueError("n_workers must be at least 1")
-    workload = compute_stream_k_workload(a, n_workers=n_workers) if a.n_blocks else None
-    return void_spmm_stream_k(a, b, workload=workload, out=out)
