@@ -91,12 +91,14 @@ def parse():
                     help="workload (default c2, the headline; c3f / c3h are config 3 with B kept in fp32 / bf16)")
     ap.add_argument("--no-per-config", dest="per_config", action="store_false",
                     help="the default run skips the other configs' extra.per_config entries")
-    ap.add_argument("--op", default="spmm", choices=["spmm", "quantize", "format", "float", "sddmm", "floor"],
+    ap.add_argument("--op", default="spmm", choices=["spmm", "quantize", "format", "float", "sddmm", "floor", "clock"],
                     help="spmm (default): the SpMM; quantize: device per-tile INT8 quantisation of the config's "
                          "A tiles; format: device CSR -> VOID tiles of the config's A; float: the float "
                          "SpMM (void_spmm) on the config's fp32 tiles and fp32 B; sddmm: the backward of A "
                          "(gradient on the config's nonzero tiles); floor: a tiny kernel and plain copies "
-                         "of c2's byte count in the same cold harness")
+                         "of c2's byte count in the same cold harness; clock: the engine clock of the SpMM's "
+                         "workgroups in the hot and cold graphs (instrumented library, built with "
+                         "`python -m void_amd.build --clock-probe`)")
     ap.add_argument("--epilogue", default=None, help="int8 epilogue (default per_block)")
     ap.add_argument("--dtype", default="f32", choices=["f32", "bf16", "f16"],
                     help="--op float / sddmm: operand dtype (bf16 / f16 run the 16-bit MFMA kernels, output in "
@@ -692,6 +694,64 @@ def traffic_summary(pmc_dir: str) -> None:
     print(json.dumps(out), flush=True)
 
 
+def bench_clock(args, dev):
+    """Engine clock of the SpMM's workgroups, hot against cold.  The
+    instrumented library makes every workgroup record s_memrealtime (100 MHz)
+    and s_memtime (shader clock) at its start and end; the clock of a
+    workgroup is the ratio of the two intervals.  Hot: a graph of K
+    back-to-back launches; cold: K x (1 GiB overwrite, launch).  The stamps
+    are those of each graph's last launch; three replays of each graph,
+    alternating."""
+    import ctypes
+    import torch
+    from void_amd import _lib, build as vbuild
+    if not vbuild.CLOCK_LIB_PATH.exists():
+        raise SystemExit(f"{vbuild.CLOCK_LIB_PATH} is missing: build it with `python -m void_amd.build --clock-probe`")
+    _lib.LIB_PATH = vbuild.CLOCK_LIB_PATH
+    prob = build_problem(args.config, dev, args.epilogue)
+    L = _lib.lib()
+    L.void_debug_set_trace.argtypes = [ctypes.c_void_p]
+    buf = torch.zeros(8 * (1 << 16), dtype=torch.int64, device=dev)
+    scratch = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    L.void_debug_set_trace(ctypes.c_void_p(buf.data_ptr()))
+    for _ in range(args.warmup):
+        prob["run"]()
+    torch.cuda.synchronize()
+
+    def capture(body):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(args.steps):
+                body(i)
+        return g
+
+    def cold(i):
+        scratch.fill_(float(i))
+        prob["run"]()
+    graphs = {"hot": capture(lambda i: prob["run"]()), "cold": capture(cold)}
+    res = {"hot": [], "cold": []}
+    for _ in range(3):
+        for name, g in graphs.items():
+            buf.zero_()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            t = buf.view(-1, 8).cpu().numpy().astype(np.int64)
+            t = t[t[:, 0] != 0]
+            mhz = (t[:, 2] - t[:, 1]) / ((t[:, 4] - t[:, 0]) * 10e-9) / 1e6
+            res[name].append({"graph_us_per_step": round(e0.elapsed_time(e1) / args.steps * 1e3, 2),
+                              "workgroups": int(len(t)), "clock_mhz_median": round(float(np.median(mhz))),
+                              "clock_mhz_p10": round(float(np.percentile(mhz, 10))),
+                              "clock_mhz_p90": round(float(np.percentile(mhz, 90)))})
+    line = {"metric": f"engine clock of the SpMM workgroups, {prob['workload']}", "unit": "MHz",
+            "value": res["hot"][-1]["clock_mhz_median"], "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "higher_is_better": True, "config": {"workload": prob["workload"]}, "extra": res}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.traffic_summary:
@@ -710,6 +770,9 @@ def main():
         return
     if args.op == "floor":
         bench_floor(args, dev)
+        return
+    if args.op == "clock":
+        bench_clock(args, dev)
         return
     if args.op != "spmm":
         bench_input_side(args, dev)

@@ -44,19 +44,29 @@ def hipcc() -> str:
     return path
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into ``void_amd/libvoid_amd.so``."""
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", *map(str, SOURCES), "-o", str(tmp)]
+# Instrumented variant for clock measurements (bench.py --op clock): every
+# SpMM workgroup records real-time and shader-clock stamps at its start and
+# end into a buffer set with void_debug_set_trace.  Not used by the product.
+CLOCK_LIB_PATH = PKG_DIR / "libvoid_amd_clock.so"
+CLOCK_FLAGS = ["-DVOID_TRACE", "-DVOID_TRACE_CLK"]
+
+
+def build(verbose: bool = False, clock_probe: bool = False) -> Path:
+    """Compile every HIP source into ``void_amd/libvoid_amd.so`` (or the
+    instrumented ``libvoid_amd_clock.so`` with clock_probe)."""
+    out = CLOCK_LIB_PATH if clock_probe else LIB_PATH
+    tmp = out.with_suffix(".so.tmp")
+    extra = CLOCK_FLAGS if clock_probe else []
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, f"-I{INCLUDE_DIR}", *map(str, SOURCES), "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout + proc.stderr)
         raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, clock_probe="--clock-probe" in sys.argv[1:]))

@@ -109,7 +109,19 @@ struct Params {
 // that nothing is stored before the kernel's loads (a store would stop the
 // compiler from using scalar loads for the read-only inputs).
 #define TRACE_DECL unsigned long long tr0 = 0, tr1 = 0, tr2 = 0, tr3 = 0, tr4 = 0, tr5 = 0, tr6 = 0, tr7 = 0
+#ifdef VOID_TRACE_CLK
+// Clock probe: point 0 also reads the shader clock counter (s_memtime) into
+// slot 1, point 4 into slot 2, so that (t2 - t1) / (t4 - t0) is the engine
+// clock over a workgroup's life; points 1 and 2 record nothing.
+#define TRACE_POINT(k)                                                                              \
+  do {                                                                                              \
+    if ((k) == 0) asm volatile("s_memrealtime %0\n\ts_memtime %1\n\ts_waitcnt lgkmcnt(0)" : "=s"(tr0), "=s"(tr1)); \
+    else if ((k) == 4) asm volatile("s_memrealtime %0\n\ts_memtime %1\n\ts_waitcnt lgkmcnt(0)" : "=s"(tr4), "=s"(tr2)); \
+    else if ((k) != 1 && (k) != 2) asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(tr##k));        \
+  } while (0)
+#else
 #define TRACE_POINT(k) asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(tr##k))
+#endif
 #define TRACE_TAG(v)                                                           \
   do {                                                                         \
     unsigned x_, h_;                                                           \
