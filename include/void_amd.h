@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define VOID_AMD_ABI_VERSION 4
+#define VOID_AMD_ABI_VERSION 5
 #define VOID_TILE 32
 
 typedef enum void_status {
@@ -98,46 +98,13 @@ typedef struct void_work_item {
   int32_t cols[VOID_ITEM_INLINE_COLS];
 } void_work_item;
 
-/* Row groups (void_rowgroup_plan): VOID_GROUP_ROWS consecutive block-rows
- * that share one pass over the union of their block columns, so that each
- * B slab of the union is gathered once for all of them.  The union is cut
- * into stages of at most VOID_STAGE_STEPS block columns ("steps") and at
- * most VOID_STAGE_TILES tiles. */
-#define VOID_GROUP_ROWS 8
-#define VOID_STAGE_STEPS 4
-#define VOID_STAGE_TILES 12
-
-/* One stage (128 bytes).  step[u] = block column (bits 0-15) | mask of the
- * group's rows with a tile there (bits 16-23, bit i = block-row row0 + i) |
- * the stage slot of the first of those tiles (bits 24-31); a step's tiles
- * take consecutive slots in row order.  tile[s] = BSR position of the tile
- * in slot s (n_tiles of them). */
-typedef struct void_stage {
-  int32_t n_steps, n_tiles;
-  int32_t step[VOID_STAGE_STEPS];
-  int32_t tile[VOID_STAGE_TILES];
-  int32_t reserved[14];
-} void_stage;
-
-/* Block-rows [row0, row0 + n_rows) and their stages [first_stage, +n_stages). */
-typedef struct void_group {
-  int32_t row0, n_rows, first_stage, n_stages;
-} void_group;
-
-/* A plan from void_streamk_plan with its items copied to device memory and,
- * optionally, a row-group plan from void_rowgroup_plan (device arrays): when
- * groups is non-null and the operands suit it (row-major B with 16-byte
- * aligned rows, no split rows), the SpMM runs the row-group kernel on it. */
+/* A plan from void_streamk_plan with its items copied to device memory. */
 typedef struct void_plan {
   const void_work_item* items; /* device array of n_items entries */
   int32_t n_items;
   int32_t n_split_tiles;
   int32_t n_slots;
   int32_t chunk_tiles;
-  const void_group* groups;    /* device array of n_groups entries, or NULL */
-  const void_stage* stages;    /* device array of the groups' stages */
-  int32_t n_groups;
-  int32_t max_group_stages;    /* most stages of any group (the kernel holds up to 64) */
 } void_plan;
 
 /* The dense operand and the output of one SpMM call. */
@@ -188,19 +155,6 @@ int void_device_info(int32_t* compute_units, int32_t* sclk_khz, int32_t* mclk_kh
 int void_streamk_plan(const int32_t* row_ptr, const int32_t* col_idx, int32_t n_block_rows,
                       int32_t chunk_tiles, void_work_item* items, int32_t capacity,
                       int32_t* n_items, int32_t* n_split_tiles, int32_t* n_slots);
-
-/* Host-side row-group planner (no counterpart in the reference; it plans
- * the B-slab reuse of the row-group kernel for the same SpMM the work items
- * describe).  Block-rows are taken VOID_GROUP_ROWS at a time in order; each
- * group's union of block columns (ascending) is cut greedily into stages.
- * row_ptr (n_block_rows + 1) and col_idx (row_ptr[n_block_rows], ascending
- * within each row) are HOST arrays; block columns must be below 65536.  On
- * VOID_ERR_CAPACITY, *n_groups / *n_stages hold the required capacities.
- * *n_steps receives the total number of union steps (B slabs per panel),
- * *max_group_stages the most stages of one group. */
-int void_rowgroup_plan(const int32_t* row_ptr, const int32_t* col_idx, int32_t n_block_rows, void_group* groups,
-                       int32_t group_capacity, void_stage* stages, int32_t stage_capacity, int32_t* n_groups,
-                       int32_t* n_stages, int64_t* n_steps, int32_t* max_group_stages);
 
 /* Bytes of device workspace a plan needs for N output columns (0 if the plan
  * splits no row).  The first n_split_tiles * n_panels int32 counters of the

@@ -292,103 +292,6 @@ def test_plan_from_workload_covers_every_tile_once():
         _runtime.plan_from_ranges(rp, ci, np.array([0]), np.array([rp[0]]), np.array([rp[2]]), 64)
 
 
-def _check_row_groups(rp, ci):
-    groups, stages, n_steps, mx = _runtime.plan_row_groups(rp, ci)
-    n_br = rp.size - 1
-    G = _lib.GROUP_ROWS
-    assert groups.shape[0] == -(-n_br // G)
-    seen = np.zeros(ci.size, dtype=np.int64)
-    total_steps = 0
-    for gi, (row0, n_rows, first, n_st) in enumerate(groups.tolist()):
-        assert row0 == G * gi and n_rows == min(G, n_br - row0)
-        rows = range(row0, row0 + n_rows)
-        union = sorted(set(int(c) for r in rows for c in ci[rp[r]:rp[r + 1]]))
-        got_cols = []
-        nxt = {r: int(rp[r]) for r in rows}  # next BSR position of each row
-        for rec in stages[first:first + n_st]:
-            k_steps, n_tiles = int(rec[0]), int(rec[1])
-            assert 1 <= k_steps <= _lib.STAGE_STEPS and 0 <= n_tiles <= _lib.STAGE_TILES
-            slot = 0
-            for u in range(k_steps):
-                w = int(rec[2 + u]) & 0xFFFFFFFF
-                col, mask, base = w & 0xFFFF, (w >> 16) & 0xFF, w >> 24
-                assert base == slot and mask != 0
-                got_cols.append(col)
-                for i in range(n_rows):
-                    present = nxt[row0 + i] < rp[row0 + i + 1] and ci[nxt[row0 + i]] == col
-                    assert bool(mask >> i & 1) == bool(present)
-                    if present:
-                        assert rec[6 + slot] == nxt[row0 + i]  # slot order: rows ascending within a step
-                        seen[nxt[row0 + i]] += 1
-                        nxt[row0 + i] += 1
-                        slot += 1
-                assert mask >> n_rows == 0
-            assert slot == n_tiles and all(t == -1 for t in rec[6 + n_tiles:6 + _lib.STAGE_TILES])
-        assert got_cols == union
-        total_steps += len(union)
-        assert n_st <= mx
-    assert np.all(seen == 1)  # every tile exactly once
-    assert n_steps == total_steps
-    assert mx == (int(groups[:, 3].max()) if groups.shape[0] else 0)
-    return groups, stages
-
-
-@pytest.mark.parametrize("seed", range(6))
-def test_rowgroup_plan_matches_brute_force(seed):
-    # Random BSR structures: ragged block-row counts (last group short),
-    # densities from empty rows to dense rows, so stages end on both the
-    # step and the tile limit.
-    rng = np.random.default_rng(seed)
-    n_br = int(rng.integers(1, 40))
-    n_bc = int(rng.integers(1, 70))
-    dens = rng.choice([0.0, 0.05, 0.3, 0.8, 1.0])
-    mask = rng.random((n_br, n_bc)) < dens
-    rp = np.concatenate([[0], np.cumsum(mask.sum(1))]).astype(np.int32)
-    ci = np.concatenate([np.nonzero(m)[0] for m in mask] + [np.zeros(0, np.int64)]).astype(np.int32)
-    _check_row_groups(rp, ci)
-
-
-def test_rowgroup_plan_c5_sharing():
-    # The FFN config: 8 rows at 25 % block density share a union step about
-    # 2.2 times, enough workgroups for the row-group kernel at a sharing
-    # threshold of 1.6; c2 (64 workgroups) never qualifies.  (By default the
-    # kernel runs on request only.)
-    c5 = cases.c5_ffn()
-    order = np.lexsort((c5.block_cols, c5.block_rows))
-    br, bc = c5.block_rows[order], c5.block_cols[order]
-    rp = np.concatenate([[0], np.cumsum(np.bincount(br, minlength=448))]).astype(np.int32)
-    groups, stages, n_steps, mx = _runtime.plan_row_groups(rp, bc.astype(np.int32))
-    assert 2.0 < len(bc) / n_steps < 2.5
-    assert tuning.use_row_groups(len(bc), n_steps, groups.shape[0], c5.N, mx, min_sharing=1.6)
-    assert not tuning.use_row_groups(len(bc), n_steps, groups.shape[0], c5.N, mx)
-    c2 = cases.c2_int8()
-    order = np.lexsort((c2.block_cols, c2.block_rows))
-    rp2 = np.concatenate([[0], np.cumsum(np.bincount(c2.block_rows, minlength=128))]).astype(np.int32)
-    g2, _, s2, m2 = _runtime.plan_row_groups(rp2, c2.block_cols[order].astype(np.int32))
-    assert not tuning.use_row_groups(len(c2.block_cols), s2, g2.shape[0], c2.N, m2, min_sharing=1.6)
-
-
-def test_rowgroup_plan_rejects_unsorted_columns():
-    rp = np.array([0, 2], np.int32)
-    ci = np.array([5, 3], np.int32)
-    with pytest.raises(_lib.VoidLibraryError):
-        _runtime.plan_row_groups(rp, ci)
-
-
-def test_row_groups_not_planned_by_default(monkeypatch):
-    # The default path never runs the row-group planner, and a plan the
-    # planner rejects (block columns beyond 16 bits) falls back quietly.
-    rp = np.array([0, 1], np.int32)
-    ci = np.array([70000], np.int32)
-    d = _runtime.DeviceBsr(tiles=torch.zeros(1, 32, 32, dtype=torch.uint8), scales=torch.ones(1),
-                           row_ptr=torch.from_numpy(rp), col_idx=torch.from_numpy(ci), row_ptr_host=rp,
-                           col_idx_host=ci, per_tensor=False, M=32, K=70001 * 32, n_blocks=1, n_block_rows=1)
-    monkeypatch.delenv("VOID_AMD_KERNEL", raising=False)
-    assert not d.use_row_groups(128) and d._row_groups is None
-    monkeypatch.setenv("VOID_AMD_KERNEL", "rg")
-    assert not d.use_row_groups(128)
-
-
 def test_b_scale_args_keep_scales_on_the_device():
     """A per-tensor B scale given as a tensor is never read back to the host:
     it becomes N device copies with the per-tensor defaults kept."""

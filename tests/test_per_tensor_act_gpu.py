@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 FP8_TOL = 2.0 ** -13
 
 
-@pytest.fixture(params=["default", "cgd3", "cgdk", "bsr", "rg"])
+@pytest.fixture(params=["default", "cgd3", "cgdk", "bsr"])
 def kernel(request, monkeypatch):
     if request.param == "default":
         monkeypatch.delenv("VOID_AMD_KERNEL", raising=False)

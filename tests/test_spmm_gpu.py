@@ -28,15 +28,14 @@ pytestmark = pytest.mark.gpu
 FP8_TOL = 2.0 ** -13
 
 
-@pytest.fixture(params=["cgd", "cgd3", "cgdk", "bsr", "rg"])
+@pytest.fixture(params=["cgd", "cgd3", "cgdk", "bsr"])
 def kernel(request, monkeypatch):
     """Runs a test on each SpMM kernel: the column-group kernel with its
     LDS-DMA ring of 4 tiles per stage (=cgd; column-major B runs the
     register-staged loop, its only default use), the 3-tile ring that unsplit
     grids beyond 512 workgroups take by default (=cgd3), the two-ring 8-wave
     workgroups that grids of at most 512 workgroups and plans with split rows
-    take (=cgdk), the general kernel (=bsr) and the row-grouped kernel (=rg,
-    where its conditions hold; elsewhere the default dispatch runs)."""
+    take (=cgdk), and the general kernel (=bsr)."""
     monkeypatch.setenv("VOID_AMD_KERNEL", request.param)
     return request.param
 
@@ -258,35 +257,6 @@ def test_c5_ffn_full_sampled_rows(gpu, monkeypatch):
     ref = oracle.gelu_tanh(oracle.i8_per_block(sub, bq, bs))
     got = out.float().cpu().numpy()[sel]
     err = np.abs(got - ref)
-    assert np.all(err <= 2.0 ** -8 * np.abs(ref) + 1e-4), err.max()
-
-
-def test_c5_row_group_kernel_full(gpu, monkeypatch):
-    """Config 5 at full size on the row-group kernel (VOID_AMD_KERNEL=rg):
-    the int32 accumulators of the whole output equal the column-group
-    kernel's (both exact), and the per-block GELU output of sampled rows
-    matches the oracle within bf16 rounding."""
-    case = cases.c5_ffn()
-    qd, A, bq, bs = _int8_setup(case, gpu)
-    bt, st = torch.from_numpy(bq).to(gpu), torch.from_numpy(bs).to(gpu)
-    monkeypatch.setenv("VOID_AMD_KERNEL", "rg")
-    assert qd.device_bsr().use_row_groups(case.N)
-    raw = void_amd.void_spmm_int8(qd, bt, b_scale=st, epilogue="raw_i32")
-    out = void_amd.void_spmm_gelu(qd, bt, b_scale=st, out_dtype=torch.bfloat16, epilogue="per_block")
-    monkeypatch.delenv("VOID_AMD_KERNEL")
-    raw_cg = void_amd.void_spmm_int8(qd, bt, b_scale=st, epilogue="raw_i32")
-    torch.cuda.synchronize()
-    assert torch.equal(raw, raw_cg)
-    rows = np.array([0, 7, 8, 100, 223, 447])
-    where = np.full(len(A.row_ptr) - 1, -1)
-    where[rows] = np.arange(len(rows))
-    keep = where[case.block_rows] >= 0
-    q = void_amd.quantize_void_tensor(cases.make_void_tensor(case, "cpu"))
-    sub = oracle.Bsr(q.values.numpy()[keep], q.scales.numpy()[keep], where[case.block_rows[keep]],
-                     case.block_cols[keep], (len(rows) * 32, case.K))
-    sel = (rows[:, None] * 32 + np.arange(32)[None, :]).reshape(-1)
-    ref = oracle.gelu_tanh(oracle.i8_per_block(sub, bq, bs))
-    err = np.abs(out.float().cpu().numpy()[sel] - ref)
     assert np.all(err <= 2.0 ** -8 * np.abs(ref) + 1e-4), err.max()
 
 

@@ -12,7 +12,7 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libvoid_amd.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # Scratch limits of void_spmm_int8_noalloc (VOID_NOALLOC_*_BYTES)
 NOALLOC_COUNTER_BYTES = 1 << 20
@@ -73,19 +73,7 @@ class Plan(ctypes.Structure):
         ("n_split_tiles", c_int32),
         ("n_slots", c_int32),
         ("chunk_tiles", c_int32),
-        ("groups", c_void_p),
-        ("stages", c_void_p),
-        ("n_groups", c_int32),
-        ("max_group_stages", c_int32),
     ]
-
-
-# Row-group plan records (void_group, void_stage) and their constants.
-GROUP_ROWS = 8
-STAGE_STEPS = 4
-STAGE_TILES = 12
-GROUP_INTS = 4
-STAGE_INTS = 32
 
 
 class DenseArgs(ctypes.Structure):
@@ -116,8 +104,6 @@ SIGNATURES = {
                                   POINTER(WorkItem), c_int32, POINTER(c_int32), POINTER(c_int32),
                                   POINTER(c_int32)]),
     "void_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
-    "void_rowgroup_plan": (c_int, [POINTER(c_int32), POINTER(c_int32), c_int32, c_void_p, c_int32, c_void_p, c_int32,
-                                   POINTER(c_int32), POINTER(c_int32), POINTER(c_int64), POINTER(c_int32)]),
     "void_spmm_int8": (c_int, [POINTER(BsrDesc), POINTER(DenseArgs), c_int32, POINTER(Plan),
                                c_void_p, c_size_t, c_void_p]),
     "void_spmm_int8_noalloc": (c_int, [POINTER(BsrDesc), POINTER(DenseArgs), c_int32, POINTER(Plan), c_void_p]),

@@ -140,39 +140,6 @@ def plan_rows(row_ptr_host: np.ndarray, chunk: int,
     return items, n_tiles.value, n_slots.value
 
 
-@dataclass
-class RowGroupPlan:
-    """A row-group plan (void_rowgroup_plan) with its records on the device."""
-    groups: torch.Tensor     # int32 [n_groups, 4] (void_group)
-    stages: torch.Tensor     # int32 [n_stages, 32] (void_stage)
-    n_groups: int
-    n_steps: int
-    max_stages: int
-    host_groups: np.ndarray
-    host_stages: np.ndarray
-
-
-def plan_row_groups(row_ptr_host: np.ndarray, col_idx_host: np.ndarray) -> Tuple[np.ndarray, np.ndarray, int, int]:
-    """Run the C row-group planner; returns (groups[g, 4], stages[s, 32], n_steps, max stages per group)."""
-    lib = _lib.lib()
-    rp = np.ascontiguousarray(row_ptr_host, dtype=np.int32)
-    ci = np.ascontiguousarray(col_idx_host, dtype=np.int32)
-    n_br = rp.size - 1
-    ng, nst, mx = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
-    nsteps = ctypes.c_int64()
-    args = (rp.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), ci.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), n_br)
-    st = lib.void_rowgroup_plan(*args, None, 0, None, 0, ctypes.byref(ng), ctypes.byref(nst), ctypes.byref(nsteps),
-                                ctypes.byref(mx))
-    if st != -5:
-        _lib.check(st, "void_rowgroup_plan")
-    groups = np.zeros((max(ng.value, 1), _lib.GROUP_INTS), dtype=np.int32)
-    stages = np.zeros((max(nst.value, 1), _lib.STAGE_INTS), dtype=np.int32)
-    st = lib.void_rowgroup_plan(*args, groups.ctypes.data, groups.shape[0], stages.ctypes.data, stages.shape[0],
-                                ctypes.byref(ng), ctypes.byref(nst), ctypes.byref(nsteps), ctypes.byref(mx))
-    _lib.check(st, "void_rowgroup_plan")
-    return groups[:ng.value], stages[:nst.value], int(nsteps.value), int(mx.value)
-
-
 def plan_from_ranges(row_ptr_host: np.ndarray, col_idx_host: np.ndarray, rows: np.ndarray, begins: np.ndarray,
                      ends: np.ndarray, max_chunk: int) -> Tuple[np.ndarray, int, int, int]:
     """Work items that run exactly the given tile ranges (BSR positions
@@ -248,7 +215,6 @@ class DeviceBsr:
     n_blocks: int
     n_block_rows: int
     plans: Dict[int, DevicePlan] = field(default_factory=dict)
-    _row_groups: Optional[RowGroupPlan] = None
     _max_row: Optional[int] = None
     _desc: Optional[_lib.BsrDesc] = None
     order: Optional[torch.Tensor] = None  # BSR position -> index of the source tile
@@ -288,35 +254,6 @@ class DeviceBsr:
             p = DevicePlan(dev_items, items.shape[0], n_tiles, n_slots, chunk, items)
             self.plans[chunk] = p
         return p
-
-    def row_groups(self) -> RowGroupPlan:
-        """The row-group plan of this matrix (built once, cached)."""
-        if self._row_groups is None:
-            g, st, n_steps, mx = plan_row_groups(self.row_ptr_host, self.col_idx_host)
-            dev = self.row_ptr.device
-            # One spare record past the end keeps every device array non-empty.
-            gd = torch.from_numpy(np.concatenate([g, np.zeros((1, g.shape[1]), np.int32)])).to(dev)
-            sd = torch.from_numpy(np.concatenate([st, np.zeros((1, st.shape[1]), np.int32)])).to(dev)
-            self._row_groups = RowGroupPlan(gd, sd, g.shape[0], n_steps, mx, g, st)
-        return self._row_groups
-
-    def use_row_groups(self, N: int) -> bool:
-        """Whether a launch with N columns takes the row-group kernel
-        (VOID_AMD_KERNEL=rg asks for it whenever the plan allows)."""
-        if self.n_blocks == 0 or self.n_block_rows == 0:
-            return False
-        force = os.environ.get("VOID_AMD_KERNEL")
-        if force and force != "rg":
-            return False
-        if force != "rg" and tuning.ROW_GROUP_MIN_SHARING == float("inf"):
-            return False  # off by default: no planning on the default path
-        try:
-            rg = self.row_groups()
-        except _lib.VoidLibraryError:
-            return False  # e.g. block columns beyond the plan's 16 bits: the column-group kernels run
-        if force == "rg":
-            return rg.max_stages <= tuning.ROW_GROUP_MAX_STAGES
-        return tuning.use_row_groups(self.n_blocks, rg.n_steps, rg.n_groups, N, rg.max_stages)
 
     def desc(self) -> _lib.BsrDesc:
         """The C descriptor of this matrix (its arrays never change: built once)."""
@@ -415,13 +352,7 @@ def launch(kind: str, dbsr: DeviceBsr, b: torch.Tensor, *, b_scale: float = 1.0,
     plan = dbsr.plan(chunk)
     stream = torch.cuda.current_stream(out.device).cuda_stream
     ws, ws_bytes = plan.workspace(N, out.device, stream)
-    if kind in ("int8", "fp8") and dbsr.use_row_groups(N):
-        rg = dbsr.row_groups()
-        cplan = _lib.Plan(items=plan.items.data_ptr(), n_items=plan.n_items, n_split_tiles=plan.n_split_tiles,
-                          n_slots=plan.n_slots, chunk_tiles=plan.chunk, groups=rg.groups.data_ptr(),
-                          stages=rg.stages.data_ptr(), n_groups=rg.n_groups, max_group_stages=rg.max_stages)
-    else:
-        cplan = plan.cplan()
+    cplan = plan.cplan()
     dense = _lib.DenseArgs(
         b=b_t.data_ptr(), ldb=ldb, b_col_major=int(col_major), N=N, b_scale=float(b_scale),
         b_scale_vec=b_scale_vec.data_ptr() if b_scale_vec is not None else None,

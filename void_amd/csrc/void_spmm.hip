@@ -99,9 +99,6 @@ struct Params {
   int32_t xcd_exact;    // grid laid out per XCD (see wg_map)
   int32_t bias_per_row;  // float kernel: bias indexed by output row
   int32_t pair_snake;    // exact layout: second half of an XCD's share reversed (see wg_map)
-  int32_t n_groups;      // row-group kernel: groups of the plan
-  const void_group* groups;
-  const void_stage* stages;
 };
 
 #ifdef VOID_TRACE
@@ -1758,7 +1755,6 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
     }
   }
   TRACE_POINT(2);
-  TRACE_POINT(3);
 
   // MFMA 32x32 result layout: lane (j, g), register r holds row
   // 8 (r / 4) + 4 g + r % 4 of column j.
@@ -1888,6 +1884,7 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
       constexpr int kChunks = kTile * esz / 16;  // 16-byte chunks per row segment
       constexpr int kRowsPer = 64 / kChunks;     // rows per store instruction
       const int ch = lane % kChunks;
+      TRACE_POINT(3);
 #pragma unroll
       for (int k = 0; k < kTile / kRowsPer; ++k) {
         const int rw = k * kRowsPer + lane / kChunks;
@@ -1939,280 +1936,6 @@ int launch_cg(const Params& p, int grid, hipStream_t stream) {
 // (16-byte aligned rows), row-major with in-register transposes (4-byte
 // aligned rows), or bytewise (anything else).
 enum Layout { kColVec, kColByte, kRowLds, kRowVec, kRowByte };
-
-// ---------------------------------------------------------------------------
-// Row-group kernel (spmm_grp_kernel): one workgroup = 16 wave64s on
-// VOID_GROUP_ROWS (8) consecutive block-rows x one 128-column panel.  Wave w
-// owns the 32-column group w % 4 of block-rows row0 + w / 4 and row0 + w / 4
-// + 4 (two 32x32 accumulators), so SIMD w % 4 holds one column group of all
-// 8 rows and every stage loads the four SIMDs alike.  The workgroup walks the union of its
-// rows' block columns, planned on the host (void_rowgroup_plan) as stages of
-// at most 4 steps and 12 tiles, through a ring of 4 stage buffers in LDS
-// filled by LDS-DMA loads:
-//  - B: each step's 4 KB slab is loaded once for all 8 rows, every wave one
-//    1 KB quarter of one step (same XOR swizzle and transposed read as the
-//    column-group kernel);
-//  - A: the stage's tiles sit in compacted slots, wave t loading slot t;
-//  - per-block scales: wave 15 loads the stage's tile scales (one per lane).
-// Every wave therefore issues a fixed number of loads per stage (2, wave 15
-// 3 with scales), so the ring's waits are fixed vmcnt counts whatever the
-// sparsity.  A wave multiplies only the steps where its row has a tile; its
-// slot is the step's first slot plus the number of lower rows present.
-// Against one slab per (tile, panel) this gathers each union slab once per
-// group: on the FFN config (25 % block density) 8 rows share a step about
-// 2.2 times on average, so the B bytes gathered into the CUs fall by that
-// factor (0.94 -> 0.41 GB; A stays at one 1 KB load per tile and panel).
-// Measured there it is nevertheless slower than the column-group kernel
-// (172 against 86 us): its loads alone run at 0.45 us per stage, but a
-// wave has only about half a tile per step to spread the step's
-// bookkeeping over (17 % more VALU and twice the SALU per tile product),
-// and the per-stage barrier of 16 waves exposes each wave's MFMA -> scaled
-// add chain, so compute takes 1.09 us per stage.  The host therefore picks
-// it only on request (VOID_AMD_KERNEL=rg).
-constexpr int kGWaves = 16;
-constexpr int kGThreads = 64 * kGWaves;
-constexpr int kGRing = 4;  // stage buffers; stages s + 1 and s + 2 load while s is multiplied
-constexpr int kGSteps = VOID_STAGE_STEPS;
-constexpr int kGTiles = VOID_STAGE_TILES;
-constexpr int kGBBytes = kGSteps * kSlotBytes;          // 16 KB of B slabs per stage
-constexpr int kGABytes = kGTiles * kTile * kTile;       // 12 KB of A tiles per stage
-constexpr int kGStageBytes = kGBBytes + kGABytes + 256;  // + one scale per lane
-constexpr int kGMaxStages = 64;                          // stage records of a group held in LDS
-constexpr int kGJunk = kGRing * kGStageBytes;            // 1 KB that the A loads of idle waves fill
-constexpr int kGRecs = kGJunk + 1024;
-constexpr int kGSmem = kGRecs + kGMaxStages * 128;
-static_assert(kGSteps * 4 == kGWaves, "one 1 KB B load (8 slab rows) per wave per stage");
-static_assert(kGTiles < kGWaves, "at most one A tile per wave per stage; the last wave loads the scales");
-static_assert(VOID_GROUP_ROWS * 2 == kGWaves, "two waves (64 columns each) per block-row");
-static_assert(VOID_STAGE_TILES >= VOID_GROUP_ROWS, "one step's tiles always fit a stage");
-static_assert(sizeof(void_stage) == 128 && sizeof(void_group) == 16, "plan records");
-
-template <int ELT, int EPI, int OUT>
-__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void spmm_grp_kernel(Params p) {
-  static_assert(ELT == kEltI8 || ELT == kEltFp8, "int8 or E4M3 tiles and B");
-  using A = Accum1<ELT, EPI>;
-  constexpr bool kInt = A::kInt;
-  constexpr bool kScales = EPI == VOID_EPI_PER_BLOCK;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kGSmem];
-  const void_stage* recs = reinterpret_cast<const void_stage*>(smem + kGRecs);
-  auto b_slab = [&](int slot, int u) -> uint8_t* { return smem + slot * kGStageBytes + u * kSlotBytes; };
-  auto a_slot = [&](int slot, int t) -> v4i* {
-    return reinterpret_cast<v4i*>(smem + slot * kGStageBytes + kGBBytes + t * (kTile * kTile));
-  };
-  auto s_slot = [&](int slot) -> float* { return reinterpret_cast<float*>(smem + slot * kGStageBytes + kGBBytes + kGABytes); };
-
-  TRACE_DECL;
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lane = tid & 63;
-  const int j = lane & 31, g = lane >> 5;
-  // Wave w: 32-column group w % 4 of the panel (so SIMD w % 4 holds one
-  // column group of every row, and each stage loads the four SIMDs alike)
-  // for rows w / 4 and w / 4 + 4 of the group.
-  const int cgw = wave & 3, r0s = wave >> 2, r1s = r0s + 4;
-
-  int grp, panel;
-  wg_tile(xcd_remap((int)blockIdx.x, (int)gridDim.x), p.n_groups, p.n_panels, p.panel_group, 1, grp, panel);
-  const void_group G = p.groups[grp];
-  const int ns = G.n_stages;
-  const void_stage* stg = p.stages + G.first_stage;
-  TRACE_POINT(0);
-  TRACE_TAG((unsigned long long)ns | ((unsigned long long)blockIdx.x << 16));
-
-  // Epilogue inputs of this lane's two columns, loaded before the ring.
-  const int cg = panel * kWaves + cgw;  // 32-column group of C
-  const int col = cg * kTile + j;        // this lane's output column
-  float sb, bias;
-  {
-    const float* sbp = p.b_scale_vec ? p.b_scale_vec : reinterpret_cast<const float*>(p.row_ptr);
-    const float* bip = p.bias ? p.bias : reinterpret_cast<const float*>(p.row_ptr);
-    const int cc = min(col, p.N - 1);
-    const float vs = sbp[p.b_scale_vec ? cc : 0];
-    const float vb = bip[p.bias ? cc : 0];
-    sb = p.b_scale_vec ? vs : p.b_scale;
-    bias = p.bias ? vb : 0.f;
-  }
-
-  const v4s da = sgpr_rsrc(p.tiles), db = sgpr_rsrc(p.b), dsc = sgpr_rsrc(p.a_scale);
-  const int ldb = (int)p.ldb;
-  const int ub = wave >> 2, qb = wave & 3;  // this wave's B load: step ub, slab rows 8 qb .. 8 qb + 7
-  const int brow = 8 * qb + (lane >> 3);
-  int cbd = panel * kPanel + 16 * ((lane & 7) ^ (brow & 7));
-  cbd = cbd < p.N ? cbd : 0;  // past N: any valid 16 bytes, never stored
-  const int voffd = brow * ldb + cbd;
-  const int kb_last = (p.K % kTile) ? p.K / kTile : -1;
-  const int voffd_last = (kb_last < 0 || brow < p.K - kb_last * kTile) ? voffd : kOutOfRange;
-  const int voff_a = j * kTile + 16 * g;
-  const int b_kstride = kTile * ldb;
-  constexpr bool kScaleWave = kScales;  // wave kGWaves - 1 also loads the stage's scales
-  const bool s_wave = kScaleWave && wave == kGWaves - 1;
-
-  // A stage record is read from LDS in one access, lane l holding word l
-  // (0 n_steps, 1 n_tiles, 2 + u step[u], 6 + t tile[t]), one iteration
-  // before it is needed; its fields are then readlanes.
-  auto rec_load = [&](int k) -> int { return reinterpret_cast<const int*>(recs + min(k, kGMaxStages - 1))[lane & 31]; };
-  auto word = [&](int v, int w) -> int { return __builtin_amdgcn_readlane(v, w); };
-  auto issue = [&](int k, int rv) {
-    const int slot = k % kGRing;
-    const int n_steps = word(rv, 0), n_tiles = word(rv, 1);
-    const int kb = word(rv, 2 + ub) & 0xffff;
-    dma_b128(db, b_slab(slot, ub) + qb * (kSlotBytes / 4), ub < n_steps ? (kb == kb_last ? voffd_last : voffd) : kOutOfRange,
-             kb * b_kstride);
-    // Waves past the stage's tiles load nothing (zeros) into the junk area,
-    // never into a live slot.
-    const bool live = wave < n_tiles;
-    const int ta = live ? word(rv, 6 + min(wave, kGTiles - 1)) : 0;
-    dma_b128(da, live ? a_slot(slot, wave) : reinterpret_cast<v4i*>(smem + kGJunk), live ? voff_a : kOutOfRange,
-             ta * (kTile * kTile));
-    if (s_wave) {
-      // Lane t < n_tiles: the scale of slot t's tile.
-      const int tl = reinterpret_cast<const int*>(recs + k)[6 + min(lane, kGTiles - 1)];
-      dma_b32(dsc, s_slot(slot), lane < n_tiles ? (p.per_tensor_a ? 0 : tl * 4) : kOutOfRange, 0);
-    }
-  };
-
-  typename A::Reg acc[2] = {};
-  // The group's stage records (128 bytes each, 8 per wave load) into LDS.
-  if (ns > 0) {
-    const v4s drec = sgpr_rsrc(stg);
-    if (wave < kGMaxStages / 8)
-      dma_b128(drec, smem + kGRecs + wave * 1024, 8 * wave + (lane >> 3) < ns ? lane * 16 : kOutOfRange, wave * 1024);
-    wait_vm<0>();
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  }
-#pragma unroll
-  for (int k = 0; k < kGRing - 1; ++k)
-    if (k < ns) issue(k, rec_load(k));
-  int rv_issue = rec_load(kGRing - 1), rv_comp = rec_load(0);
-  TRACE_POINT(1);
-  for (int s = 0; s < ns; ++s) {
-    const int ahead = min(ns - 1, s + kGRing - 2) - s;  // stages issued after s
-    if (s_wave) wait_stages<3>(ahead);
-    else wait_stages<2>(ahead);
-    // Every wave's part of stage s has landed, and every wave has finished
-    // reading stage s - 1, whose buffer the next issue overwrites.
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (s + kGRing - 1 < ns) issue(s + kGRing - 1, rv_issue);
-    rv_issue = rec_load(s + kGRing);
-    const int rv = rv_comp;
-    rv_comp = rec_load(s + 1);
-    const int slot = s % kGRing;
-    const int n_steps = word(rv, 0);
-#pragma unroll
-    for (int u = 0; u < kGSteps; ++u) {
-      const int w = word(rv, 2 + u);
-      const int mask = u < n_steps ? (w >> 16) & 0xff : 0;
-      const int pm = ((mask >> r0s) & 1) | (((mask >> r1s) & 1) << 1);  // this wave's rows with a tile
-      if (pm) {
-        const int base = (int)((unsigned)w >> 24);
-        Frag1 f;
-        f.b = read_tr(b_slab(slot, u), cgw, j, g);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          if ((pm >> h) & 1) {
-            const int rr = h ? r1s : r0s;
-            const int sl = base + __builtin_popcount(mask & ((1 << rr) - 1));
-            f.a = a_slot(slot, sl)[lane];
-            if constexpr (kInt) {
-              A::step(acc[h], f, 0.f);
-            } else {
-              const float sc = kScales ? s_slot(slot)[sl] : 1.f;
-              A::fold(acc[h], A::prod(f), sc);
-            }
-          }
-        }
-      }
-    }
-  }
-  // The ring is idle from here: its LDS stages the output blocks.
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  TRACE_POINT(2);
-
-  constexpr int esz = (OUT == VOID_DT_F32 || OUT == VOID_DT_I32) ? 4 : 2;
-  const Rsrc rc = make_rsrc(p.c);
-  const int ldc = (int)p.ldc;
-  constexpr int kRowB = kTile * esz + 16;  // padded row stride: the two half waves hit other banks
-  static_assert(kGWaves * kTile * kRowB <= kGJunk, "output staging fits the ring");
-  uint8_t* stg_lds = smem + wave * (kTile * kRowB);
-  const bool aligned = ((reinterpret_cast<uintptr_t>(p.c) | (uintptr_t)(ldc * esz)) & 15) == 0;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int rs = h ? r1s : r0s;
-    if (rs >= G.n_rows) break;
-    const int row = G.row0 + rs;
-    float mul = 1.f;
-    if constexpr (EPI == VOID_EPI_ROW_MEAN) {
-      // int_quant.py:519-526: S = sum fl(s_a * s_b) in tile order over the
-      // block-row, then S / n (s_b per column: one per lane).
-      const int rb = p.row_ptr[row], re = p.row_ptr[row + 1];
-      float S = 0.f;
-      for (int t0 = rb; t0 < re; t0 += 64) {
-        const int n = min(64, re - t0);
-        const float mine = p.per_tensor_a ? p.a_scale[0] : p.a_scale[t0 + min(lane, n - 1)];
-        for (int q = 0; q < n; ++q) S = __fadd_rn(S, __fmul_rn(bcast(mine, q), sb));
-      }
-      mul = re > rb ? __fdiv_rn(S, (float)(re - rb)) : 0.f;
-    } else if constexpr (EPI == VOID_EPI_PER_BLOCK) {
-      mul = sb;
-    }
-    const int row0 = row * kTile;
-    float xv[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float x = 0.f;
-      if constexpr (EPI != VOID_EPI_RAW_I32) x = __fmul_rn((float)acc[h][r], mul);
-      if (p.bias) x = __fadd_rn(x, bias);
-      xv[r] = x;
-    }
-    if constexpr (OUT != VOID_DT_I32) activate_all(xv, p.activation);
-    const bool full = row0 + kTile <= p.M && cg * kTile + kTile <= p.N;
-    if (full && aligned) {
-      // Row-major through the wave's own LDS area, then 16-byte stores that
-      // each cover 8 (f32, i32) or 16 (bf16, f16) full row segments.
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rr = 8 * (r >> 2) + (r & 3) + 4 * g;
-        uint8_t* d = stg_lds + rr * kRowB + j * esz;
-        if constexpr (OUT == VOID_DT_F32) *reinterpret_cast<float*>(d) = xv[r];
-        else if constexpr (OUT == VOID_DT_I32) *reinterpret_cast<int*>(d) = (int)acc[h][r];
-        else *reinterpret_cast<uint16_t*>(d) = (uint16_t)(OUT == VOID_DT_BF16 ? f32_to_bf16_bits(xv[r]) : f32_to_f16_bits(xv[r]));
-      }
-      constexpr int kChunks = kTile * esz / 16;
-      constexpr int kRowsPer = 64 / kChunks;
-      const int ch = lane % kChunks;
-#pragma unroll
-      for (int k = 0; k < kTile / kRowsPer; ++k) {
-        const int rw = k * kRowsPer + lane / kChunks;
-        const v4i v = *reinterpret_cast<const v4i*>(stg_lds + rw * kRowB + ch * 16);
-        __builtin_amdgcn_raw_buffer_store_b128(v, rc, ((row0 + rw) * ldc + cg * kTile) * esz + ch * 16, 0, kStoreStream);
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rr = 8 * (r >> 2) + (r & 3) + 4 * g;
-        if (row0 + rr < p.M && col < p.N) {
-          const int off = ((row0 + rr) * ldc + col) * esz;
-          if constexpr (OUT == VOID_DT_F32) __builtin_amdgcn_raw_buffer_store_b32(__float_as_int(xv[r]), rc, off, 0, 0);
-          else if constexpr (OUT == VOID_DT_I32) __builtin_amdgcn_raw_buffer_store_b32((int)acc[h][r], rc, off, 0, 0);
-          else {
-            const uint32_t hb = OUT == VOID_DT_BF16 ? f32_to_bf16_bits(xv[r]) : f32_to_f16_bits(xv[r]);
-            __builtin_amdgcn_raw_buffer_store_b16((unsigned short)hb, rc, off, 0, 0);
-          }
-        }
-      }
-    }
-  }
-  TRACE_POINT(4);
-  TRACE_FLUSH();
-}
-
-template <int ELT, int EPI, int OUT>
-int launch_grp(const Params& p, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((spmm_grp_kernel<ELT, EPI, OUT>), dim3(grid), dim3(kGThreads), 0, stream, p);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(VOID_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
-  return VOID_OK;
-}
 
 // ---------------------------------------------------------------------------
 // Float kernel (void_spmm_f32): fp32 tiles times fp32 B, the reference's
@@ -2662,9 +2385,9 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
     }
   }
 
-  // The column-group and row-grouped kernels address every operand with
+  // The column-group kernel addresses every operand with
   // 31-bit buffer offsets; larger operands and the other B layouts use
-  // spmm_bsr_kernel.  VOID_AMD_KERNEL=bsr / cg / cgd / rg forces a kernel
+  // spmm_bsr_kernel.  VOID_AMD_KERNEL=bsr / cg / cgd forces a kernel
   // where it applies (for comparisons and tests; cg is the register-staged
   // column-group loop, cgd its LDS-DMA ring, the default).
   const int esz = (d->out_dtype == VOID_DT_BF16 || d->out_dtype == VOID_DT_F16) ? 2 : 4;
@@ -2674,52 +2397,10 @@ int run(int elt, const void_bsr_desc* a, const void_dense_args* d, int32_t epilo
   const char* force = getenv("VOID_AMD_KERNEL");
   const bool force_bsr = force && strcmp(force, "bsr") == 0;
   const bool force_cg = force && strcmp(force, "cg") == 0;
-  const bool force_rg = force && strcmp(force, "rg") == 0;
   const bool force_deep = force && strcmp(force, "cgd3") == 0;
   const bool force_pair = force && strcmp(force, "cgdk") == 0;
   const bool offsets_ok = (int64_t)a->n_blocks * kTile * kTile < kLim && b_span < kLim &&
                           (int64_t)a->M * d->ldc * esz < kLim;
-
-  // Row-group kernel: when the plan carries a row-group plan (the host
-  // builds one where rows share many block columns) and B is row-major with
-  // 16-byte aligned rows.  VOID_AMD_KERNEL=rg asks for it (the host then
-  // builds the row-group plan whatever the sharing); any other forced
-  // kernel skips it.
-  const bool grp_ok = plan->groups && plan->stages && plan->n_groups > 0 && layout == kRowLds && offsets_ok &&
-                      plan->max_group_stages <= kGMaxStages && (elt == kEltI8 || elt == kEltFp8) &&
-                      (!force || force_rg);
-  if (grp_ok) {
-    if (plan->n_groups != (a->n_block_rows + VOID_GROUP_ROWS - 1) / VOID_GROUP_ROWS)
-      return fail(VOID_ERR_ARG, "row-group plan has %d groups for %d block-rows", plan->n_groups, a->n_block_rows);
-    Params q = p;
-    q.groups = plan->groups;
-    q.stages = plan->stages;
-    q.n_groups = plan->n_groups;
-    q.n_items = plan->n_groups;
-    const int64_t ggrid = (int64_t)plan->n_groups * n_panels;
-    if (ggrid > 0x7fffffff) return fail(VOID_ERR_ARG, "grid too large");
-    auto go = [&](auto elt_c, auto epi_c) -> int {
-      constexpr int E = decltype(elt_c)::value, P = decltype(epi_c)::value;
-      if constexpr (P == VOID_EPI_RAW_I32) {
-        return launch_grp<E, P, VOID_DT_I32>(q, (int)ggrid, stream);
-      } else {
-        switch (d->out_dtype) {
-          case VOID_DT_F32: return launch_grp<E, P, VOID_DT_F32>(q, (int)ggrid, stream);
-          case VOID_DT_BF16: return launch_grp<E, P, VOID_DT_BF16>(q, (int)ggrid, stream);
-          case VOID_DT_F16: return launch_grp<E, P, VOID_DT_F16>(q, (int)ggrid, stream);
-          default: return fail(VOID_ERR_UNSUPPORTED, "out_dtype %d not supported with this epilogue", d->out_dtype);
-        }
-      }
-    };
-    using I8 = std::integral_constant<int, kEltI8>;
-    using F8 = std::integral_constant<int, kEltFp8>;
-    if (elt == kEltFp8) return go(F8{}, std::integral_constant<int, VOID_EPI_PER_BLOCK>{});
-    switch (epilogue) {
-      case VOID_EPI_RAW_I32: return go(I8{}, std::integral_constant<int, VOID_EPI_RAW_I32>{});
-      case VOID_EPI_ROW_MEAN: return go(I8{}, std::integral_constant<int, VOID_EPI_ROW_MEAN>{});
-      default: return go(I8{}, std::integral_constant<int, VOID_EPI_PER_BLOCK>{});
-    }
-  }
 
   const bool cg_ok = (layout == kRowLds || layout == kColVec) && plan->chunk_tiles <= kCgMaxTiles && offsets_ok &&
                      !force_bsr;
@@ -2932,72 +2613,6 @@ int void_streamk_plan(const int32_t* row_ptr, const int32_t* col_idx, int32_t n_
   return VOID_OK;
 }
 
-int void_rowgroup_plan(const int32_t* row_ptr, const int32_t* col_idx, int32_t n_block_rows, void_group* groups,
-                       int32_t group_capacity, void_stage* stages, int32_t stage_capacity, int32_t* n_groups,
-                       int32_t* n_stages, int64_t* n_steps, int32_t* max_group_stages) {
-  g_err[0] = 0;
-  if (!row_ptr || !n_groups || !n_stages || !n_steps || !max_group_stages || n_block_rows < 0)
-    return fail(VOID_ERR_ARG, "bad row-group planner arguments");
-  if (n_block_rows > 0 && row_ptr[n_block_rows] > 0 && !col_idx) return fail(VOID_ERR_ARG, "null col_idx");
-  std::vector<void_group> gs;
-  std::vector<void_stage> ss;
-  int64_t steps_total = 0;
-  constexpr int G = VOID_GROUP_ROWS;
-  for (int32_t r0 = 0; r0 < n_block_rows; r0 += G) {
-    const int nr = std::min<int32_t>(G, n_block_rows - r0);
-    int32_t pos[G], end[G];
-    for (int i = 0; i < nr; ++i) {
-      pos[i] = row_ptr[r0 + i];
-      end[i] = row_ptr[r0 + i + 1];
-      if (end[i] < pos[i]) return fail(VOID_ERR_ARG, "row_ptr decreases at row %d", r0 + i);
-    }
-    void_group grp{r0, nr, (int32_t)ss.size(), 0};
-    void_stage st{};
-    auto flush = [&]() {
-      if (st.n_steps > 0) {
-        for (int t = st.n_tiles; t < VOID_STAGE_TILES; ++t) st.tile[t] = -1;
-        ss.push_back(st);
-        grp.n_stages += 1;
-      }
-      st = void_stage{};
-    };
-    int prev = -1;
-    while (true) {
-      // Next union column: the smallest head among the rows.
-      int32_t c = INT32_MAX;
-      for (int i = 0; i < nr; ++i)
-        if (pos[i] < end[i]) c = std::min(c, col_idx[pos[i]]);
-      if (c == INT32_MAX) break;
-      if (c <= prev) return fail(VOID_ERR_ARG, "block columns not ascending in a row of group %d", r0 / G);
-      if (c > 0xffff) return fail(VOID_ERR_UNSUPPORTED, "block column %d beyond the row-group plan's 16 bits", c);
-      prev = c;
-      int mask = 0, cnt = 0;
-      for (int i = 0; i < nr; ++i)
-        if (pos[i] < end[i] && col_idx[pos[i]] == c) {
-          mask |= 1 << i;
-          ++cnt;
-        }
-      if (st.n_steps == VOID_STAGE_STEPS || st.n_tiles + cnt > VOID_STAGE_TILES) flush();
-      st.step[st.n_steps++] = c | (mask << 16) | (st.n_tiles << 24);
-      for (int i = 0; i < nr; ++i)
-        if (mask >> i & 1) st.tile[st.n_tiles++] = pos[i]++;
-      ++steps_total;
-    }
-    flush();
-    gs.push_back(grp);
-  }
-  *n_groups = (int32_t)gs.size();
-  *n_stages = (int32_t)ss.size();
-  *n_steps = steps_total;
-  int32_t mx = 0;
-  for (const void_group& x : gs) mx = std::max(mx, x.n_stages);
-  *max_group_stages = mx;
-  if (!groups || !stages || group_capacity < (int32_t)gs.size() || stage_capacity < (int32_t)ss.size())
-    return fail(VOID_ERR_CAPACITY, "row-group planner needs %zu groups and %zu stages", gs.size(), ss.size());
-  std::memcpy(groups, gs.data(), gs.size() * sizeof(void_group));
-  std::memcpy(stages, ss.data(), ss.size() * sizeof(void_stage));
-  return VOID_OK;
-}
 
 size_t void_workspace_bytes(int32_t n_split_tiles, int32_t n_slots, int32_t N) {
   if (n_split_tiles <= 0 || N <= 0) return 0;

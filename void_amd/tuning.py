@@ -70,27 +70,6 @@ def select_chunk(kind: str, n_blocks: int, N: int, max_row: int = 0) -> int:
     return min(cg_max, max(MIN_SPLIT_CHUNK, int(math.ceil(per_slot * factor))))
 
 
-# Row-group kernel (B slabs shared by 8 block-rows): one 16-wave workgroup per
-# CU, so it needs at least two rounds of workgroups, and it could pay only
-# where the rows share many block columns.  Measured on the FFN config (2.2
-# tiles per union step) it runs at half the column-group kernel's speed
-# (172 against 86 us), so the default sharing threshold is never met and it
-# runs on request only (VOID_AMD_KERNEL=rg).
-ROW_GROUP_MIN_WORKGROUPS = 2 * GFX950_CUS
-ROW_GROUP_MIN_SHARING = float("inf")
-ROW_GROUP_MAX_STAGES = 64
-
-
-def use_row_groups(n_blocks: int, n_steps: int, n_groups: int, N: int, max_stages: int,
-                   min_sharing: float = ROW_GROUP_MIN_SHARING) -> bool:
-    """Whether the row-group kernel runs: enough (group, panel) workgroups,
-    at least min_sharing tiles per union step, and every group's stage
-    records within what the kernel holds."""
-    if n_steps <= 0 or max_stages > ROW_GROUP_MAX_STAGES:
-        return False
-    return n_groups * n_panels(max(N, 1)) >= ROW_GROUP_MIN_WORKGROUPS and n_blocks / n_steps >= min_sharing
-
-
 # A column-major B (X.t() of token-major activations) runs the register-staged
 # column-group loop, whose 16-byte loads from one column each use a quarter
 # of a 128-byte line; the LDS-DMA ring reads row-major B in whole lines.  When
