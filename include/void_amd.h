@@ -142,6 +142,12 @@ int void_panel_width(void);
  * state the peaks it divides by.  Returns VOID_OK or VOID_ERR_HIP. */
 int void_device_info(int32_t* compute_units, int32_t* sclk_khz, int32_t* mclk_khz, int32_t* bus_bits);
 
+/* The id of the HIP graph capture that `stream` is in, or 0 when it is not
+ * capturing (hipStreamGetCaptureInfo).  No counterpart in the reference; the
+ * Python layer uses it to give the launches of one capture on one stream a
+ * single split-row workspace.  Returns VOID_OK or VOID_ERR_HIP. */
+int void_stream_capture_id(hipStream_t stream, unsigned long long* id);
+
 /* Host-side Stream-K planner.  Replaces compute_stream_k_workload
  * (void/stream_k.py:36-110): every block-row becomes one item, except rows
  * with more than chunk_tiles tiles, which are split into ceil(n/chunk_tiles)

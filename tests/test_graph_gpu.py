@@ -148,9 +148,10 @@ def test_graph_int8_float_b(gpu):
 
 def test_graph_two_captures_of_one_split_plan(gpu):
     """Two graphs captured from one split plan, the second replayed first and
-    then the two alternately: each capture owns a workspace zeroed inside
-    its own graph, so no replay depends on another graph's zeroing or shares
-    its arrival counters."""
+    then the two alternately: each capture owns a workspace (the first the
+    plan's spare, zeroed before the capture; the second one zeroed inside its
+    own graph), so no replay depends on another graph's zeroing or shares its
+    arrival counters."""
     case = cases.uniform_blocks(1024, 2048, 256, 900, seed=5)
     q, bt, st = _int8(case, gpu)
     fn = lambda: void_amd.void_spmm_int8(q, bt, b_scale=st, epilogue="per_block", chunk_tiles=3)
@@ -165,6 +166,9 @@ def test_graph_two_captures_of_one_split_plan(gpu):
             outs.append(fn())
         graphs.append(g)
     torch.cuda.synchronize()
+    plan = next(p for p in q.device_bsr().plans.values() if p.n_split_tiles > 0)
+    ws = plan.capture_workspaces[-2:]
+    assert len(ws) == 2 and ws[0].data_ptr() != ws[1].data_ptr() and not plan.capture_spares
     other = _other(gpu)
     for k in (1, 0, 1, 0, 0, 1):
         outs[k].zero_()
@@ -183,3 +187,30 @@ def test_graph_two_captures_of_one_split_plan(gpu):
         graphs[1].replay()
     torch.cuda.synchronize()
     assert torch.equal(_bits(outs[0]), _bits(ref)) and torch.equal(_bits(outs[1]), _bits(ref))
+
+
+def test_graph_split_plan_captured_first(gpu):
+    """A split plan whose very first call is captured (no eager call before
+    it, so no spare workspace): the captured fill clears the counters, and
+    every replay, and an eager call after them, give the eager result."""
+    case = cases.uniform_blocks(1024, 2048, 256, 900, seed=6)
+    q, bt, st = _int8(case, gpu)
+    fn = lambda: void_amd.void_spmm_int8(q, bt, b_scale=st, epilogue="per_block", chunk_tiles=4)
+    q.device_bsr().plan(4)  # the plan exists, no workspace yet
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    torch.cuda.synchronize()
+    other = _other(gpu)
+    results = []
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        other()
+        torch.cuda.synchronize()
+        results.append(out.clone())
+    ref = fn()
+    torch.cuda.synchronize()
+    for r in results:
+        assert torch.equal(_bits(r), _bits(ref))

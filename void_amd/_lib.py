@@ -100,6 +100,7 @@ SIGNATURES = {
     "void_last_error": (c_char_p, []),
     "void_panel_width": (c_int, []),
     "void_device_info": (c_int, [POINTER(c_int32), POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
+    "void_stream_capture_id": (c_int, [c_void_p, POINTER(ctypes.c_ulonglong)]),
     "void_streamk_plan": (c_int, [POINTER(c_int32), POINTER(c_int32), c_int32, c_int32,
                                   POINTER(WorkItem), c_int32, POINTER(c_int32), POINTER(c_int32),
                                   POINTER(c_int32)]),

@@ -32,6 +32,9 @@ _OUT_CODES = {
 # Streams whose eager split-row workspaces a plan keeps (least recently used
 # first out).
 MAX_STREAM_WORKSPACES = 8
+# Largest split-row workspace of which a plan keeps a zeroed spare for the
+# next HIP graph capture.
+MAX_SPARE_WORKSPACE = 64 << 20
 
 
 @dataclass
@@ -44,6 +47,8 @@ class DevicePlan:
     host_items: np.ndarray       # int32 [n_items, 32] copy, for inspection
     workspaces: "OrderedDict[Tuple[int, int], torch.Tensor]" = field(default_factory=OrderedDict)
     capture_workspaces: List[torch.Tensor] = field(default_factory=list)
+    capture_spares: Dict[int, torch.Tensor] = field(default_factory=dict)  # nbytes -> zeroed, for the next capture
+    capture_by_id: Dict[Tuple[int, int, int], torch.Tensor] = field(default_factory=dict)  # (capture, stream, nbytes)
     ws_sizes: Dict[int, int] = field(default_factory=dict)  # N -> void_workspace_bytes
     _cplan: Optional["_lib.Plan"] = None
 
@@ -53,6 +58,11 @@ class DevicePlan:
             self._cplan = _lib.Plan(items=self.items.data_ptr(), n_items=self.n_items,
                                     n_split_tiles=self.n_split_tiles, n_slots=self.n_slots, chunk_tiles=self.chunk)
         return self._cplan
+
+    def counter_bytes(self, N: int) -> int:
+        """Bytes of split-row arrival counters at the start of the workspace
+        (n_split_tiles x n_panels int32, rounded up to 256 bytes)."""
+        return (self.n_split_tiles * tuning.n_panels(max(N, 1)) * 4 + 255) // 256 * 256
 
     def workspace(self, N: int, device: torch.device,
                   stream: Optional[int] = None) -> Tuple[Optional[torch.Tensor], int]:
@@ -65,20 +75,36 @@ class DevicePlan:
         stream handle, torch's current stream of ``device`` by default.
 
         Eager launches reuse one workspace per stream, the last
-        ``MAX_STREAM_WORKSPACES`` streams being kept.  A launch under HIP graph
-        capture gets a workspace of its own, zeroed by a fill kernel captured
-        into the same graph, so that every graph clears and owns its counters
-        and graphs replayed on different streams never share them; it is kept
-        for the lifetime of the plan (one per capture)."""
+        ``MAX_STREAM_WORKSPACES`` streams being kept.  Under HIP graph capture
+        each (capture, stream) gets a workspace of its own, its counters zeroed
+        by a fill kernel captured into the same graph before its first launch,
+        so that every graph clears and owns its counters and graphs replayed on
+        different streams never share them; the launches of one capture on one
+        stream run in order and share it.  It is kept for the lifetime of the
+        plan.  Only the counters are cleared: the partial blocks are always
+        written before they are read.  The first eager launch of a size also
+        prepares one spare workspace (up to MAX_SPARE_WORKSPACE bytes), zeroed
+        and synchronised once, which the next capture takes as its own with no
+        fill kernel in the graph."""
         nbytes = self.ws_sizes.get(N)
         if nbytes is None:
             nbytes = self.ws_sizes[N] = int(_lib.lib().void_workspace_bytes(self.n_split_tiles, self.n_slots, N))
         if nbytes == 0:
             return None, 0
         if torch.cuda.is_current_stream_capturing():
-            ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
-            ws.zero_()
-            self.capture_workspaces.append(ws)
+            raw = stream if stream is not None else torch.cuda.current_stream(device).cuda_stream
+            cid = ctypes.c_ulonglong(0)
+            _lib.check(_lib.lib().void_stream_capture_id(ctypes.c_void_p(int(raw)), ctypes.byref(cid)),
+                       "void_stream_capture_id")
+            key = (int(cid.value), int(raw), nbytes)
+            ws = self.capture_by_id.get(key)
+            if ws is None:
+                ws = self.capture_spares.pop(nbytes, None)
+                if ws is None:
+                    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+                    ws[:self.counter_bytes(N)].zero_()
+                self.capture_by_id[key] = ws
+                self.capture_workspaces.append(ws)
             return ws, nbytes
         if stream is None:
             stream = torch.cuda.current_stream(device).cuda_stream
@@ -88,8 +114,14 @@ class DevicePlan:
             # Counters must start at zero; every launch leaves them at zero.
             # The zeroing runs on the stream that will use the workspace.
             ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
-            _zero_on_stream(ws, int(stream), device)
+            _zero_on_stream(ws[:self.counter_bytes(N)], int(stream), device)
             self.workspaces[key] = ws
+            if nbytes <= MAX_SPARE_WORKSPACE and nbytes not in self.capture_spares:
+                spare = torch.empty(nbytes, dtype=torch.uint8, device=device)
+                spare[:self.counter_bytes(N)].zero_()
+                # Zeroed before any graph can use it, whatever stream replays it.
+                torch.cuda.current_stream(device).synchronize()
+                self.capture_spares[nbytes] = spare
             while len(self.workspaces) > MAX_STREAM_WORKSPACES:
                 # The oldest stream's workspace is freed; the caching allocator
                 # keeps its memory until the work queued on that stream is done.

@@ -2536,6 +2536,17 @@ const char* void_last_error(void) { return g_err; }
 
 int void_panel_width(void) { return kPanel; }
 
+int void_stream_capture_id(hipStream_t stream, unsigned long long* id) {
+  g_err[0] = 0;
+  if (!id) return fail(VOID_ERR_ARG, "null id");
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  unsigned long long cid = 0;
+  const hipError_t e = hipStreamGetCaptureInfo(stream, &st, &cid);
+  if (e != hipSuccess) return fail(VOID_ERR_HIP, "hipStreamGetCaptureInfo: %s", hipGetErrorString(e));
+  *id = st == hipStreamCaptureStatusActive ? cid : 0;
+  return VOID_OK;
+}
+
 int void_device_info(int32_t* compute_units, int32_t* sclk_khz, int32_t* mclk_khz, int32_t* bus_bits) {
   g_err[0] = 0;
   if (!compute_units || !sclk_khz || !mclk_khz || !bus_bits) return fail(VOID_ERR_ARG, "null output pointer");
