@@ -214,3 +214,33 @@ def test_graph_split_plan_captured_first(gpu):
     torch.cuda.synchronize()
     for r in results:
         assert torch.equal(_bits(r), _bits(ref))
+
+
+def test_graph_calls_of_one_capture_share_a_workspace(gpu):
+    """Several calls of one split plan in one capture, on one stream, with
+    different B operands: they run in order and share one workspace (each
+    launch leaves the counters at zero for the next), and every replay
+    gives each call's eager result."""
+    case = cases.uniform_blocks(1024, 2048, 256, 900, seed=7)
+    q, bt, st = _int8(case, gpu)
+    bt2 = torch.flip(bt, dims=[0]).contiguous()
+    f1 = lambda: void_amd.void_spmm_int8(q, bt, b_scale=st, epilogue="per_block", chunk_tiles=5)
+    f2 = lambda: void_amd.void_spmm_int8(q, bt2, b_scale=st, epilogue="per_block", chunk_tiles=5)
+    r1, r2 = f1().clone(), f2().clone()
+    torch.cuda.synchronize()
+    plan = q.device_bsr().plans[5]
+    assert plan.n_split_tiles > 0
+    n_before = len(plan.capture_workspaces)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        o1, o2, o3 = f1(), f2(), f1()
+    assert len(plan.capture_workspaces) == n_before + 1
+    other = _other(gpu)
+    for _ in range(3):
+        for o in (o1, o2, o3):
+            o.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        other()
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(o1), _bits(r1)) and torch.equal(_bits(o2), _bits(r2)) and torch.equal(_bits(o3), _bits(r1))
