@@ -34,6 +34,10 @@ HIPCC_FLAGS = [
     # Packed fp32 VALU forms are kept out of generated code on this pool.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
+    # The column-group kernel's first five argument dwords (work-list address
+    # and the packed grid layout) arrive preloaded in SGPRs, so that its first
+    # work-item read does not wait for a kernel-argument load.
+    "-mllvm", "-amdgpu-kernarg-preload-count=5",
 ]
 
 

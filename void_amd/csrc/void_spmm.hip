@@ -240,6 +240,29 @@ __device__ __forceinline__ bool wg_map(const Params& p, int& item, int& panel) {
   return true;
 }
 
+// wg_map on the layout fields packed into three scalar kernel arguments
+// (map_word: xcd_exact | pair_snake << 1 | item_piles << 2 | panel_group << 8),
+// which the column-group kernel takes ahead of Params so that they can be
+// preloaded into SGPRs with the work list's address: its first work-item read
+// then waits for no kernel-argument load.
+__device__ __forceinline__ bool wg_map_args(int map_word, int n_items, int n_panels, int& item, int& panel) {
+  const int h = (int)blockIdx.x;
+  const int piles = (map_word >> 2) & 63, pg = map_word >> 8;
+  if (map_word & 1) {
+    const int x = h & 7, s = h >> 3;
+    int k = s / pg;
+    panel = (x / piles) * pg + (s - k * pg);
+    if (map_word & 2) {
+      const int share = (n_items + piles - 1) / piles, half = (share + 1) >> 1;
+      k = k < half ? k : share - 1 - (k - half);
+    }
+    item = k * piles + x % piles;
+    return item < n_items;
+  }
+  wg_tile(xcd_remap(h, (int)gridDim.x), n_items, n_panels, pg, piles, item, panel);
+  return true;
+}
+
 // Split-row fix-up ordering (all three kernels).  The protocol uses no
 // release/acquire fences (at agent scope on gfx950 they write back and
 // invalidate the XCD's whole L2); it is ordered by completion instead:
@@ -1140,7 +1163,8 @@ constexpr int kStoreStream = 2 | 16;
 
 template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false, int RT = kDmaTiles, int KS = 1>
 __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
-    DMA ? (KS > 1 ? 4 : dma_waves_per_eu(RT)) : 2, DMA ? (KS > 1 ? 4 : dma_waves_per_eu(RT)) : 2))) void spmm_cg_kernel(Params p) {
+    DMA ? (KS > 1 ? 4 : dma_waves_per_eu(RT)) : 2, DMA ? (KS > 1 ? 4 : dma_waves_per_eu(RT)) : 2))) void
+    spmm_cg_kernel(const void_work_item* __restrict__ items, int map_word, int map_items, int map_panels, Params p) {
   static_assert(!(DMA && BCOL), "the LDS-DMA ring is for row-major B");
   static_assert(KS == 1 || (DMA && KS == 2), "the two-ring split is for the LDS-DMA ring");
   using A = Accum1<ELT, EPI>;
@@ -1179,8 +1203,8 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
   const int j = lane & 31, g = lane >> 5;
 
   int item_idx, panel;
-  if (!wg_map(p, item_idx, panel)) return;
-  const void_work_item* itp = p.items + item_idx;
+  if (!wg_map_args(map_word, map_items, map_panels, item_idx, panel)) return;
+  const void_work_item* itp = items + item_idx;
   const v4i* colv = reinterpret_cast<const v4i*>(itp->cols);
   const v4i cq0 = colv[0], cq1 = colv[1], cq2 = colv[2], cq3 = colv[3];
   __builtin_amdgcn_sched_barrier(0);
@@ -1925,7 +1949,9 @@ __global__ __launch_bounds__(kThreads * KS) __attribute__((amdgpu_waves_per_eu(
 
 template <int ELT, int EPI, int OUT, bool BCOL, bool DMA = false, int RT = kDmaTiles, int KS = 1>
 int launch_cg(const Params& p, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((spmm_cg_kernel<ELT, EPI, OUT, BCOL, DMA, RT, KS>), dim3(grid), dim3(kThreads * KS), 0, stream, p);
+  const int map_word = p.xcd_exact | p.pair_snake << 1 | p.item_piles << 2 | p.panel_group << 8;
+  hipLaunchKernelGGL((spmm_cg_kernel<ELT, EPI, OUT, BCOL, DMA, RT, KS>), dim3(grid), dim3(kThreads * KS), 0, stream,
+                     p.items, map_word, p.n_items, p.n_panels, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(VOID_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
   return VOID_OK;
