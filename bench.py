@@ -91,14 +91,17 @@ def parse():
                     help="workload (default c2, the headline; c3f / c3h are config 3 with B kept in fp32 / bf16)")
     ap.add_argument("--no-per-config", dest="per_config", action="store_false",
                     help="the default run skips the other configs' extra.per_config entries")
-    ap.add_argument("--op", default="spmm", choices=["spmm", "quantize", "format", "float", "sddmm", "floor", "clock"],
+    ap.add_argument("--op", default="spmm",
+                    choices=["spmm", "quantize", "format", "float", "sddmm", "floor", "clock", "phases"],
                     help="spmm (default): the SpMM; quantize: device per-tile INT8 quantisation of the config's "
                          "A tiles; format: device CSR -> VOID tiles of the config's A; float: the float "
                          "SpMM (void_spmm) on the config's fp32 tiles and fp32 B; sddmm: the backward of A "
                          "(gradient on the config's nonzero tiles); floor: a tiny kernel and plain copies "
                          "of c2's byte count in the same cold harness; clock: the engine clock of the SpMM's "
                          "workgroups in the hot and cold graphs (instrumented library, built with "
-                         "`python -m void_amd.build --clock-probe`)")
+                         "`python -m void_amd.build --clock-probe`); phases: per-workgroup phase timeline of "
+                         "the SpMM in the cold and hot graphs (instrumented library, built with "
+                         "`python -m void_amd.build --phase-probe`)")
     ap.add_argument("--epilogue", default=None, help="int8 epilogue (default per_block)")
     ap.add_argument("--dtype", default="f32", choices=["f32", "bf16", "f16"],
                     help="--op float / sddmm: operand dtype (bf16 / f16 run the 16-bit MFMA kernels, output in "
@@ -752,6 +755,69 @@ def bench_clock(args, dev):
     print(json.dumps(line), flush=True)
 
 
+def bench_phases(args, dev):
+    """Per-workgroup phase timeline of the SpMM (the column-group kernel's LDS-DMA
+    ring).  The instrumented library makes workgroup thread 0 record
+    s_memrealtime (100 MHz) at: 0 the work item read, 1 the first stage
+    issued, 5 the first stage landed, 6 the tile loop done, 2 the two rings'
+    hand-off done (split rows: the fix-up too), 3 the epilogue staged, 4 the
+    stores issued.  Cold: K x (1 GiB overwrite, launch); hot: K back-to-back
+    launches; the stamps are those of each graph's last launch, three replays
+    of each, alternating.  Phases are medians (and 10th / 90th percentiles)
+    over workgroups, in microseconds."""
+    import ctypes
+    import torch
+    from void_amd import _lib, build as vbuild
+    if not vbuild.PHASE_LIB_PATH.exists():
+        raise SystemExit(f"{vbuild.PHASE_LIB_PATH} is missing: build it with `python -m void_amd.build --phase-probe`")
+    _lib.LIB_PATH = vbuild.PHASE_LIB_PATH
+    prob = build_problem(args.config, dev, args.epilogue)
+    L = _lib.lib()
+    L.void_debug_set_trace.argtypes = [ctypes.c_void_p]
+    buf = torch.zeros(8 * (1 << 16), dtype=torch.int64, device=dev)
+    scratch = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    L.void_debug_set_trace(ctypes.c_void_p(buf.data_ptr()))
+    for _ in range(args.warmup):
+        prob["run"]()
+    torch.cuda.synchronize()
+
+    def capture(body):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(args.steps):
+                body(i)
+        return g
+
+    def cold(i):
+        scratch.fill_(float(i))
+        prob["run"]()
+    graphs = {"hot": capture(lambda i: prob["run"]()), "cold": capture(cold)}
+    names = [("issue", 0, 1), ("first_stage_landed", 0, 5), ("loop", 5, 6), ("hand_off", 6, 2),
+             ("epilogue_math_staging", 2, 3), ("store_issue", 3, 4), ("life", 0, 4)]
+    res = {"hot": [], "cold": []}
+    for _ in range(3):
+        for name, g in graphs.items():
+            buf.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            t = buf.view(-1, 8).cpu().numpy().astype(np.int64)
+            t = t[t[:, 0] != 0]
+            full = t[t[:, 4] != 0]  # workgroups that ran the staged epilogue (not split chunks)
+            q = lambda x: [round(float(np.percentile(x, p)) / 100, 2) for p in (10, 50, 90)]
+            t0 = t[:, 0].min()
+            ends = np.max(t[:, [2, 4, 6]], axis=1)
+            rec = {"workgroups": int(len(t)), "start_spread_us": q(t[:, 0] - t0),
+                   "span_us": round(float(ends.max() - t0) / 100, 2)}
+            for nm, a, b in names:
+                rec[nm + "_us"] = q(full[:, b] - full[:, a])
+            res[name].append(rec)
+    line = {"metric": f"SpMM phase timeline, {prob['workload']}", "unit": "us", "value": res["cold"][-1]["span_us"],
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": False,
+            "config": {"workload": prob["workload"]}, "extra": res}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.traffic_summary:
@@ -773,6 +839,9 @@ def main():
         return
     if args.op == "clock":
         bench_clock(args, dev)
+        return
+    if args.op == "phases":
+        bench_phases(args, dev)
         return
     if args.op != "spmm":
         bench_input_side(args, dev)

@@ -53,14 +53,20 @@ def hipcc() -> str:
 # end into a buffer set with void_debug_set_trace.  Not used by the product.
 CLOCK_LIB_PATH = PKG_DIR / "libvoid_amd_clock.so"
 CLOCK_FLAGS = ["-DVOID_TRACE", "-DVOID_TRACE_CLK"]
+# Instrumented variant for phase timelines (bench.py --op phases): every SpMM
+# workgroup records s_memrealtime at its phase boundaries.  Not used by the
+# product.
+PHASE_LIB_PATH = PKG_DIR / "libvoid_amd_phase.so"
+PHASE_FLAGS = ["-DVOID_TRACE"]
 
 
-def build(verbose: bool = False, clock_probe: bool = False) -> Path:
+def build(verbose: bool = False, clock_probe: bool = False, phase_probe: bool = False) -> Path:
     """Compile every HIP source into ``void_amd/libvoid_amd.so`` (or the
-    instrumented ``libvoid_amd_clock.so`` with clock_probe)."""
-    out = CLOCK_LIB_PATH if clock_probe else LIB_PATH
+    instrumented ``libvoid_amd_clock.so`` with clock_probe,
+    ``libvoid_amd_phase.so`` with phase_probe)."""
+    out = CLOCK_LIB_PATH if clock_probe else PHASE_LIB_PATH if phase_probe else LIB_PATH
     tmp = out.with_suffix(".so.tmp")
-    extra = CLOCK_FLAGS if clock_probe else []
+    extra = CLOCK_FLAGS if clock_probe else PHASE_FLAGS if phase_probe else []
     cmd = [hipcc(), *HIPCC_FLAGS, *extra, f"-I{INCLUDE_DIR}", *map(str, SOURCES), "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -73,4 +79,4 @@ def build(verbose: bool = False, clock_probe: bool = False) -> Path:
 
 
 if __name__ == "__main__":
-    print(build(verbose=True, clock_probe="--clock-probe" in sys.argv[1:]))
+    print(build(verbose=True, clock_probe="--clock-probe" in sys.argv[1:], phase_probe="--phase-probe" in sys.argv[1:]))
