@@ -258,7 +258,7 @@ def time_gpu(prob, steps: int, warmup: int, flush: bool):
     """Kernel time from HIP-graph replays, so host launch overhead is excluded.
 
     cold: a graph of `steps` x (overwrite a 1 GiB buffer, SpMM) minus a graph of
-    `steps` x (overwrite), median over 7 alternating pairs of replays -- the
+    `steps` x (overwrite), median over 11 alternating pairs of replays -- the
     SpMM then always starts with L2 and the Infinity Cache holding none of its
     inputs; hot: a graph of `steps` x SpMM.
     Both graphs are bracketed by events on the capture-replay stream with a
@@ -300,14 +300,15 @@ def time_gpu(prob, steps: int, warmup: int, flush: bool):
     if flush:
         g_cold = capture(cold_body)
         g_flush = capture(lambda i: scratch.fill_(float(i)))
-        g_cold.replay()
-        g_flush.replay()
+        for _ in range(3):  # settle clocks and caches on a fresh box
+            g_cold.replay()
+            g_flush.replay()
         torch.cuda.synchronize()
         # Replays of the two graphs alternate and the median of the pairwise
         # differences is kept: the overwrites take ~15x the SpMM, so drift in
         # their speed between two separate averages would swamp the result.
         diffs = []
-        for _ in range(7):
+        for _ in range(11):
             diffs.append(replay_ms(g_cold, reps=1) - replay_ms(g_flush, reps=1))
         cold = sorted(diffs)[len(diffs) // 2] / steps
     wall = time.perf_counter() - t0
