@@ -316,6 +316,24 @@ def test_split_dealing_geometries(gpu, N, kernel):
     assert np.array_equal(raw.cpu().numpy(), oracle.i8_acc(A, bq))
 
 
+@pytest.mark.parametrize("N", [2048, 4096])
+@pytest.mark.parametrize("chunk", [None, 3])
+def test_wide_panel_groups(gpu, N, chunk, kernel):
+    """N of 2048 and 4096 (16 and 32 panels): each XCD's share of the grid
+    covers a group of 2 or 4 panels, in the per-XCD layout both for a
+    one-round unsplit grid (second half of each share reversed) and for split
+    rows (dealt shares): every (item, panel) must run exactly once."""
+    case = cases.uniform_blocks(320 if chunk is None else 640, 1024, N, 150, seed=17)
+    qd, A, bq, bs = _int8_setup(case, gpu)
+    bt = torch.from_numpy(bq).to(gpu)
+    raw = void_amd.void_spmm_int8(qd, bt, b_scale=torch.from_numpy(bs).to(gpu), epilogue="raw_i32", chunk_tiles=chunk)
+    torch.cuda.synchronize()
+    plans = qd.device_bsr().plans
+    if chunk is not None:
+        assert any(p.n_split_tiles > 0 for p in plans.values()), "the case must split rows"
+    assert np.array_equal(raw.cpu().numpy(), oracle.i8_acc(A, bq))
+
+
 def test_determinism_split(gpu):
     case = cases.uniform_blocks(512, 4096, 384, 1200, seed=5)
     qd, A, bq, bs = _int8_setup(case, gpu)
